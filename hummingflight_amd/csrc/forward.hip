@@ -1,0 +1,84 @@
+// forward.hip -- MoE-layer orchestration on the device (GLMForward::moeLayer,
+// glm_forward.cpp:509-661): router -> selection -> expert SwiGLU -> weighted
+// combine + shared expert, all on one stream with no host round trip.
+#include "hf_api_internal.h"
+
+namespace hf {
+
+int gu_blocks() { return env_int("HFMOE_GU_BLOCKS", g.num_cus * 2); }
+int dn_blocks() { return env_int("HFMOE_DN_BLOCKS", g.num_cus * 2); }
+
+static int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s) {
+    if (!dbg) return HFMOE_OK;
+    const Cfg& c = g.cfg;
+    hipError_t e = hipSuccess;
+    if (dbg->logits_dev && e == hipSuccess)
+        e = hipMemcpyAsync(dbg->logits_dev, g.ws.logits, sizeof(float) * (size_t)T * c.E,
+                           hipMemcpyDeviceToDevice, s);
+    if (dbg->idx_dev && e == hipSuccess)
+        e = hipMemcpyAsync(dbg->idx_dev, g.ws.idx, sizeof(int) * (size_t)T * c.k,
+                           hipMemcpyDeviceToDevice, s);
+    if (dbg->weight_dev && e == hipSuccess)
+        e = hipMemcpyAsync(dbg->weight_dev, g.ws.wts, sizeof(float) * (size_t)T * c.k,
+                           hipMemcpyDeviceToDevice, s);
+    if (T > 1 && g.gws.offsets) {
+        if (dbg->offsets_dev && e == hipSuccess)
+            e = hipMemcpyAsync(dbg->offsets_dev, g.gws.offsets, sizeof(int) * (size_t)(c.E + 1),
+                               hipMemcpyDeviceToDevice, s);
+        if (dbg->perm_dev && e == hipSuccess)
+            e = hipMemcpyAsync(dbg->perm_dev, g.gws.perm, sizeof(int) * (size_t)T * c.k,
+                               hipMemcpyDeviceToDevice, s);
+    }
+    return e == hipSuccess ? HFMOE_OK : fail_hip(e, "debug copies");
+}
+
+int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg) {
+    const Cfg& c = g.cfg;
+    const int nslots = c.k + c.n_shared;
+    Pending p;
+    prof_begin(p, "router", s);
+    hipError_t e = launch_router_t1(x, L.dev, c, g.ws.logits, g.ws.idx, g.ws.wts, g.ws.counter, s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "router launch");
+    prof_begin(p, "expert_gateup", s);
+    e = launch_gateup_t1(x, L.dev, c, g.ws.idx, g.ws.h, nslots, gu_blocks(), s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "gate/up launch");
+    prof_begin(p, "expert_down", s);
+    e = launch_down_t1(g.ws.h, L.dev, c, g.ws.idx, g.ws.wts, nullptr, out, nslots, dn_blocks(), s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "down launch");
+    return copy_debug(dbg, 1, s);
+}
+
+}  // namespace hf
+
+namespace hf {
+
+// Multi-token forward, token by token over the decode kernels.  Every token
+// re-streams its experts' weights, so this is the correctness path for small T
+// until the dispatch + grouped kernels take over.
+int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                    const hfmoe_route_debug* dbg) {
+    const Cfg& c = g.cfg;
+    const int nslots = c.k + c.n_shared;
+    Pending p;
+    prof_begin(p, "router_tokens", s);
+    hipError_t e = launch_router_tokens(x, T, L.dev, c, g.ws.logits, g.ws.idx, g.ws.wts, s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "router launch");
+    for (int t = 0; t < T; ++t) {
+        e = launch_gateup_t1(x + (size_t)t * c.d, L.dev, c, g.ws.idx + (size_t)t * c.k, g.ws.h,
+                             nslots, gu_blocks(), s);
+        if (e != hipSuccess) return fail_hip(e, "gate/up launch");
+        e = launch_down_t1(g.ws.h, L.dev, c, g.ws.idx + (size_t)t * c.k, g.ws.wts + (size_t)t * c.k,
+                           nullptr, out + (size_t)t * c.d, nslots, dn_blocks(), s);
+        if (e != hipSuccess) return fail_hip(e, "down launch");
+    }
+    return copy_debug(dbg, T, s);
+}
+
+int grouped_workspace_alloc() { return HFMOE_OK; }
+void grouped_workspace_free() {}
+
+}  // namespace hf

@@ -1,0 +1,137 @@
+// hf_api_internal.h -- library state shared by the C-ABI translation units.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "../../include/hfmoe.h"
+#include "hf_kernels.h"
+
+namespace hf {
+
+struct Workspace {
+    float* logits = nullptr;     // [maxT, E]
+    int* idx = nullptr;          // [maxT, k]
+    float* wts = nullptr;        // [maxT, k]
+    float* h = nullptr;          // [k + n_shared, I]  (T = 1 path)
+    unsigned int* counter = nullptr;
+    float* x_io = nullptr;       // [d]  host-contract staging
+    float* out_io = nullptr;     // [d]
+    float* tmp = nullptr;        // [2, maxT, d] (mlp block: normed x, MoE out)
+};
+
+// Buffers of the multi-token (dispatch + grouped) path.
+struct GroupedWorkspace {
+    int* counts = nullptr;       // [E]
+    int* offsets = nullptr;      // [E + 1]
+    int* perm = nullptr;         // [maxT*k]
+    int* tile_info = nullptr;    // scheduling scratch
+    uint16_t* xb = nullptr;      // [maxT*k, d] x gathered in expert order, BF16 hi
+    uint16_t* xl = nullptr;      // [maxT*k, d] BF16 lo residual
+    uint16_t* hb = nullptr;      // [maxT*k, I] h hi
+    uint16_t* hl = nullptr;      // [maxT*k, I] h lo
+    float* y = nullptr;          // [maxT*k, d] per-pair expert outputs
+    uint16_t* sxb = nullptr;     // shared expert: x BF16 hi/lo in token order
+    uint16_t* sxl = nullptr;
+    uint16_t* shb = nullptr;     // shared h hi/lo [maxT, S*I]
+    uint16_t* shl = nullptr;
+    float* sy = nullptr;         // shared output [maxT, d]
+    unsigned int* flags = nullptr;
+    size_t bytes = 0;
+};
+
+struct LayerState {
+    int location = HFMOE_EXPERTS_DEVICE;
+    LayerDev dev{};
+    const uint16_t** etab_dev = nullptr;
+    std::vector<const uint16_t*> host_experts;  // 3*E as registered
+    const uint16_t* norm_w = nullptr;
+};
+
+struct Pending {
+    const char* name = nullptr;
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+// Staging pool of the streamed-expert path: HBM slots that receive selected
+// experts from pinned host RAM on the copy stream.
+struct StreamPool {
+    int slots = 0;
+    size_t slot_bytes = 0;
+    uint16_t* base = nullptr;
+    std::vector<hipEvent_t> copied;   // per slot: H2D done (copy stream)
+    std::vector<hipEvent_t> consumed; // per slot: last kernel reading it done
+    std::vector<uint64_t> key;        // (layer << 32 | expert) resident in slot, or ~0
+    std::vector<uint64_t> last_use;
+    uint64_t clock = 0;
+    int* idx_host = nullptr;          // pinned [k] selected experts readback
+    float* w_host = nullptr;
+    const uint16_t** etab_host = nullptr;  // pinned [3*k] slot pointers for the table
+    const uint16_t** etab_dev = nullptr;   // device [3*k] slot pointers of this call
+    int* iota_dev = nullptr;               // device [k] = 0..k-1 (slot order)
+    float* shared_out = nullptr;           // device [d] shared-expert output
+    hipEvent_t routed = nullptr;
+    uint64_t hits = 0, misses = 0;
+};
+
+struct State {
+    bool inited = false;
+    bool configured = false;
+    int device = -1;
+    int num_cus = 0;
+    size_t total_mem = 0;
+    char name[256] = {0};
+    hipStream_t stream = nullptr;
+    hipStream_t copy_stream = nullptr;
+    Cfg cfg{};
+    int max_tokens = 1;
+    uint64_t vram_budget = 0;
+    std::map<int, LayerState> layers;
+    Workspace ws;
+    GroupedWorkspace gws;
+    StreamPool pool;
+    // profiling / telemetry
+    bool prof_on = false;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, std::pair<int64_t, double>> kstats;
+    uint64_t pcie_bytes = 0;
+    uint64_t gpu_active_ns = 0;
+    std::string last_error;
+};
+
+extern State g;
+
+int fail(int code, const char* fmt, ...);
+int fail_hip(hipError_t e, const char* what);
+int require_init();
+int require_cfg();
+int env_int(const char* name, int dflt);
+hipStream_t pick_stream(void* s);
+void prof_begin(Pending& p, const char* name, hipStream_t s);
+void prof_end(Pending& p, hipStream_t s);
+void prof_drain();
+
+// forward.hip
+int gu_blocks();
+int dn_blocks();
+int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg);
+int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                    const hfmoe_route_debug* dbg);
+int grouped_workspace_alloc();
+void grouped_workspace_free();
+// streamed.hip
+int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hipStream_t s,
+                        const hfmoe_route_debug* dbg);
+void stream_pool_release();
+// misc kernels
+hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
+                          hipStream_t s);
+hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s);
+
+}  // namespace hf

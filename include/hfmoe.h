@@ -1,0 +1,161 @@
+/*
+ * hfmoe.h -- C-ABI of the MI355X (gfx950) MoE-block library, libhfmoe.so.
+ *
+ * Drop-in boundary for HummingFlight's MoE block.  The engine keeps
+ * GLMForward::moeLayer(int layer, const float* input, float* output)
+ * (src/model/glm_forward.h:93) and its weight handles (TensorLocation /
+ * ExpertWeights / LayerWeights, src/model/weight_index.h:14-68) and calls
+ * these entry points; the per-expert GPU plugin surface of
+ * src/compute/cuda_backend.h:23-90 is covered one for one.
+ *
+ * Conventions (cuda_backend.h:56-62 uses bool; here):
+ *   - every entry point returns an int status, HFMOE_OK (0) on success; the
+ *     engine shim maps a non-zero status to the reference's `false`, which
+ *     makes moeLayer restart the layer on its own CPU path
+ *     (glm_forward.cpp:594-602).  The library itself has no CPU compute path.
+ *   - hfmoe_last_error() describes the most recent failure.
+ *   - no C++ exceptions cross this boundary; no torch types appear in it.
+ *   - pointers named *_dev are HBM addresses; *_host are host addresses.
+ *   - not thread-safe: one caller thread, as the reference's generation
+ *     thread (cuda_backend.cpp:366 is a process-global singleton too).
+ *   - `stream` arguments are hipStream_t values; NULL selects the library's
+ *     own stream (default priority).
+ */
+#ifndef HFMOE_H
+#define HFMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HFMOE_OK = 0,
+    HFMOE_ERR_NO_DEVICE = 1,
+    HFMOE_ERR_NOT_INITIALIZED = 2,
+    HFMOE_ERR_INVALID_ARGUMENT = 3,
+    HFMOE_ERR_UNSUPPORTED = 4,
+    HFMOE_ERR_OUT_OF_MEMORY = 5,
+    HFMOE_ERR_NOT_REGISTERED = 6,
+    HFMOE_ERR_HIP = 7
+};
+
+/* Where a layer's routed-expert weights live. */
+enum {
+    HFMOE_EXPERTS_DEVICE = 0,      /* HBM-resident, read in place */
+    HFMOE_EXPERTS_HOST_PINNED = 1  /* pinned host RAM; only selected experts are
+                                      copied to HBM (hipMemcpyAsync, side stream) */
+};
+
+/* MoE fields of ModelConfig (src/model/config.h:49-58,78) plus budgets. */
+typedef struct hfmoe_config {
+    int32_t hidden;               /* hiddenSize */
+    int32_t moe_intermediate;     /* moeIntermediateSize (one routed expert) */
+    int32_t n_routed_experts;     /* numLocalExperts, <= 1024 */
+    int32_t num_experts_per_tok;  /* numExpertsPerTok, 1..8 */
+    int32_t n_group;              /* 1 = flat noaux_tc (the reference's rule) */
+    int32_t topk_group;           /* groups kept when n_group > 1 (config.h:58) */
+    int32_t n_shared_experts;     /* nSharedExperts; shared inter = n * moe_intermediate */
+    int32_t norm_topk_prob;       /* normTopkProb */
+    float routed_scaling_factor;  /* routedScalingFactor */
+    float rms_norm_eps;           /* rmsNormEps */
+    uint64_t vram_budget_bytes;   /* AdaptiveConfig::vramBudgetBytes
+                                     (src/runtime/runtime_config.h:62); bounds the
+                                     streamed-expert staging pool; 0 = default */
+    int32_t max_tokens;           /* largest T of one forward call (workspace) */
+    int32_t reserved;
+} hfmoe_config;
+
+/* One MoE layer's tensors (LayerWeights / ExpertWeights,
+ * src/model/weight_index.h:28-36,58-67).  BF16 values are raw uint16 bits. */
+typedef struct hfmoe_layer_weights {
+    const uint16_t* router_dev;       /* mlp.gate.weight      [E, hidden] */
+    const float* score_bias_dev;      /* e_score_correction_bias F32 [E], or NULL */
+    const uint16_t* shared_gate_dev;  /* shared_experts.gate_proj [S*I, hidden] */
+    const uint16_t* shared_up_dev;    /* shared_experts.up_proj   [S*I, hidden] */
+    const uint16_t* shared_down_dev;  /* shared_experts.down_proj [hidden, S*I] */
+    const uint16_t* const* experts;   /* host array of 3*E pointers, expert e at
+                                         [3e] gate [I,hidden], [3e+1] up [I,hidden],
+                                         [3e+2] down [hidden,I]; HBM or pinned host
+                                         addresses per experts_location */
+    const uint16_t* post_attention_norm_dev; /* RMSNorm weight BF16 [hidden] or NULL
+                                                (used by hfmoe_mlp_block) */
+    int32_t experts_location;         /* HFMOE_EXPERTS_* */
+    int32_t reserved;
+} hfmoe_layer_weights;
+
+/* Optional routing outputs of a forward call (HBM pointers, any may be NULL). */
+typedef struct hfmoe_route_debug {
+    float* logits_dev;     /* [T, E] router GEMV before sigmoid */
+    int32_t* idx_dev;      /* [T, k] selected experts, descending biased score */
+    float* weight_dev;     /* [T, k] normalised, scaled routing weights */
+    int32_t* offsets_dev;  /* [E+1] dispatch offsets (T > 1 paths) */
+    int32_t* perm_dev;     /* [T*k] pair ids t*k+r ordered by (expert, pair) */
+} hfmoe_route_debug;
+
+/* ---- device lifetime (cuda_backend.h:23-34) ---- */
+int hfmoe_init(int device);                      /* cudaInit */
+void hfmoe_shutdown(void);                       /* cudaShutdown */
+int hfmoe_available(void);                       /* gpuAvailable: 1 after init */
+int hfmoe_device_name(char* buf, size_t len);    /* cudaDeviceName */
+size_t hfmoe_device_memory_mb(void);             /* cudaDeviceMemoryMB */
+const char* hfmoe_last_error(void);
+
+/* ---- MoE layer (GLMForward::moeLayer, glm_forward.h:93) ---- */
+int hfmoe_configure(const hfmoe_config* cfg);
+int hfmoe_register_layer(int layer, const hfmoe_layer_weights* w);
+/* out_dev[T, hidden] = MoE(x_dev[T, hidden]), FP32 in and out, device pointers. */
+int hfmoe_moe_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
+int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out_dev,
+                            void* stream, const hfmoe_route_debug* dbg);
+/* The moeLayer contract itself: one token, host FP32 buffers, synchronous. */
+int hfmoe_moe_layer(int layer, const float* input_host, float* output_host);
+/* h_dev[T, hidden] += MoE(RMSNorm(h_dev)) -- the MoE half of a decoder layer
+ * (glm_forward.cpp:785-796). */
+int hfmoe_mlp_block(int layer, float* h_dev, int32_t T, void* stream);
+
+/* ---- per-expert plugin surface (cuda_backend.h:64-90) ---- */
+int hfmoe_expert_cache_config(int capacity, int staging_depth); /* gpuExpertCacheConfig */
+void hfmoe_expert_cache_shutdown(void);                         /* gpuExpertCacheShutdown */
+int hfmoe_experts_enabled(void);                                /* gpuExpertsEnabled */
+int hfmoe_expert_stage(int layer, int expert_id, const uint16_t* w_host, int hidden,
+                       int inter);                              /* gpuExpertStage */
+int hfmoe_expert_ffn(int layer, int expert_id, const float* x_host, float* out_host,
+                     int hidden, int inter);                    /* gpuExpertFFN */
+int hfmoe_self_test(void);                                      /* cudaExpertSelfTest */
+
+/* ---- buffers and synthetic data (no counterpart: harness plumbing) ---- */
+int hfmoe_malloc(void** ptr_dev, size_t bytes);
+int hfmoe_free(void* ptr_dev);
+int hfmoe_host_alloc(void** ptr_host, size_t bytes);   /* pinned host memory */
+int hfmoe_host_free(void* ptr_host);
+int hfmoe_memcpy_h2d(void* dst_dev, const void* src_host, size_t bytes);
+int hfmoe_memcpy_d2h(void* dst_host, const void* src_dev, size_t bytes);
+int hfmoe_memcpy_d2d(void* dst_dev, const void* src_dev, size_t bytes);
+int hfmoe_memset(void* ptr_dev, int value, size_t bytes);
+int hfmoe_synchronize(void);
+/* Seeded counter-based N(mean, std) tensors in HBM (BF16 bits or F32). */
+int hfmoe_fill_normal_bf16(uint16_t* dst_dev, uint64_t n, uint64_t seed, uint64_t tensor,
+                           uint64_t first, float mean, float std);
+int hfmoe_fill_normal_f32(float* dst_dev, uint64_t n, uint64_t seed, uint64_t tensor,
+                          uint64_t first, float mean, float std);
+
+/* ---- telemetry (InferenceStats gpuActiveNs / pcieBytes,
+ *      src/engine/inference_stats.h:86-93) ---- */
+typedef struct hfmoe_kernel_stat {
+    char name[32];
+    int64_t launches;
+    double total_ms;   /* sum of hipEvent-measured durations on the launch stream */
+} hfmoe_kernel_stat;
+
+int hfmoe_profile_enable(int on);                 /* per-kernel hipEvent timing */
+int hfmoe_profile_read(hfmoe_kernel_stat* out, int max_entries, int* n_entries);
+int hfmoe_profile_reset(void);
+int hfmoe_stats(uint64_t* pcie_bytes, uint64_t* gpu_active_ns);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

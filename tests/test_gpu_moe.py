@@ -1,0 +1,264 @@
+"""GPU parity of the MoE block against the CPU oracle, through the C-ABI.
+
+Bar: expert indices bit-exact given the same router
+logits; outputs within 1e-2 relative + 2e-3 absolute of the oracle, which is
+itself bit-exact with the reference's moeLayer (test_oracle.py).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from hummingflight_amd import capi, synth
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 2e-3
+
+
+def assert_close(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    tol = ATOL + RTOL * np.abs(ref)
+    bad = np.flatnonzero(err > tol)
+    assert bad.size == 0, (f"{what}: {bad.size} elements outside tolerance, worst at {bad[0]}: "
+                           f"got {got.flat[bad[0]]} ref {ref.flat[bad[0]]}")
+
+
+def ulp_diff(a, b):
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+SMALL = dict(hidden=2048, inter=1024, n_experts=64, top_k=8)
+FULL = dict(hidden=6144, inter=2048, n_experts=256, top_k=8)
+
+
+class Run:
+    """One configured layer on the device plus its oracle twin."""
+
+    def __init__(self, dims, n_group=1, topk_group=1, seed=1, T=1, layer=0, n_shared=1,
+                 on_host=False, with_norm=False, bias=None, max_tokens=None):
+        self.shape = synth.LayerShape(n_group=n_group, topk_group=topk_group, n_shared=n_shared, **dims)
+        capi.call("hfmoe_configure", self.shape.config(max_tokens=max_tokens or T))
+        self.dev = synth.DeviceLayer(self.shape, layer=layer, seed=seed, experts_on_host=on_host,
+                                     with_norm=with_norm, bias=bias)
+        self.spec = O.LayerSpec(n_group=n_group, topk_group=topk_group, n_shared=n_shared, seed=seed,
+                                layer=layer, bias_override=bias, **dims)
+        self.ref = O.SyntheticLayer(self.spec)
+        self.T = T
+        self.layer = layer
+
+    def forward(self, x_dev, T=None):
+        T = T or self.T
+        s = self.shape
+        out = capi.DeviceBuffer(T * s.hidden * 4)
+        lg = capi.DeviceBuffer(T * s.n_experts * 4)
+        idx = capi.DeviceBuffer(T * s.top_k * 4)
+        w = capi.DeviceBuffer(T * s.top_k * 4)
+        off = capi.DeviceBuffer((s.n_experts + 1) * 4)
+        perm = capi.DeviceBuffer(T * s.top_k * 4)
+        dbg = capi.RouteDebug(lg.ptr, idx.ptr, w.ptr, off.ptr, perm.ptr)
+        capi.call("hfmoe_moe_forward_debug", self.layer, x_dev.ptr, T, out.ptr, None, C.byref(dbg))
+        capi.call("hfmoe_synchronize")
+        res = dict(out=out.download(np.float32, T * s.hidden).reshape(T, s.hidden),
+                   logits=lg.download(np.float32, T * s.n_experts).reshape(T, s.n_experts),
+                   idx=idx.download(np.int32, T * s.top_k).reshape(T, s.top_k),
+                   w=w.download(np.float32, T * s.top_k).reshape(T, s.top_k),
+                   offsets=off.download(np.int32, s.n_experts + 1),
+                   perm=perm.download(np.int32, T * s.top_k))
+        for b in (out, lg, idx, w, off, perm):
+            b.free()
+        return res
+
+    def check_token(self, x, res, t):
+        """Selection given the GPU's logits, then the output given that selection."""
+        ridx, rw = self.ref.route(res["logits"][t])
+        assert res["idx"][t].tolist() == ridx.tolist(), f"token {t}: selection differs"
+        assert ulp_diff(res["w"][t], rw).max() <= 2, f"token {t}: weights differ"
+        ref = self.ref.combine(x, ridx, rw)
+        assert_close(res["out"][t], ref, f"token {t} output")
+        return ridx, ref
+
+    def free(self):
+        self.dev.free()
+
+
+def test_device_generator_matches_oracle(hf):
+    n = 1 << 16
+    buf = capi.DeviceBuffer(n * 4)
+    for seed, tensor, mean, std, first in [(1, 5, 0.0, 0.02, 0), (9, (3 << 40) | 77, 1.0, 0.05, 12345),
+                                           (4, 2, 0.0, 1.0, 1 << 33)]:
+        synth.fill_bf16(buf.ptr, n, seed, tensor, mean, std, first)
+        got = buf.download(np.uint16, n)
+        assert np.array_equal(got, O.fill_bf16(n, seed, tensor, mean, std, first=first))
+        synth.fill_f32(buf.ptr, n, seed, tensor, mean, std, first)
+        got = buf.download(np.float32, n)
+        assert np.array_equal(got.view(np.uint32), O.fill_f32(n, seed, tensor, mean, std, first=first).view(np.uint32))
+    buf.free()
+
+
+@pytest.mark.parametrize("n_group,topk_group", [(1, 1), (8, 4)])
+def test_decode_small_layer(hf, n_group, topk_group):
+    r = Run(SMALL, n_group=n_group, topk_group=topk_group, seed=5)
+    x = synth.make_x_dev(1, SMALL["hidden"], seed=5)
+    res = r.forward(x)
+    xh = x.download(np.float32, SMALL["hidden"])
+    ridx, _ = r.check_token(xh, res, 0)
+    # The oracle's own logits (serial FP32 GEMV) pick the same experts here.
+    out, lg, idx, w = r.ref.forward(xh)
+    assert np.max(np.abs(lg - res["logits"][0])) < 1e-4
+    assert idx.tolist() == ridx.tolist()
+    assert_close(res["out"][0], out, "end-to-end")
+    x.free()
+    r.free()
+
+
+def test_decode_matches_reference_golden_small(hf, golden):
+    cases = [c for c in golden["moe_layer"] if c["name"] == "small"]
+    c0 = cases[0]
+    r = Run(SMALL, seed=c0["seed"])
+    xs = O.make_x(len(cases), SMALL["hidden"], c0["seed"])
+    for c in cases:
+        x = capi.DeviceBuffer.of(xs[c["token"]])
+        res = r.forward(x)
+        assert res["idx"][0].tolist() == c["idx"]
+        ref = np.array(c["out"], np.uint32).view(np.float32)
+        assert_close(res["out"][0], ref, f"reference golden token {c['token']}")
+        x.free()
+    r.free()
+
+
+def test_decode_full_shape_grouped(hf):
+    # d=6144, 256 experts, 8 groups keep 4, top-8 (the benchmark layer).
+    r = Run(FULL, n_group=8, topk_group=4, seed=2)
+    x = synth.make_x_dev(1, FULL["hidden"], seed=2)
+    res = r.forward(x)
+    xh = x.download(np.float32, FULL["hidden"])
+    ridx, _ = r.check_token(xh, res, 0)
+    assert len(set(i // 32 for i in ridx.tolist())) <= 4
+    x.free()
+    r.free()
+
+
+def test_decode_matches_reference_golden_full(hf, golden):
+    c = [c for c in golden["moe_layer"] if c["name"] == "full"][0]
+    r = Run(FULL, seed=c["seed"])
+    x = capi.DeviceBuffer.of(O.make_x(1, FULL["hidden"], c["seed"])[0])
+    res = r.forward(x)
+    assert res["idx"][0].tolist() == c["idx"]
+    assert_close(res["out"][0], np.array(c["out"], np.uint32).view(np.float32), "full-shape golden")
+    x.free()
+    r.free()
+
+
+def test_decode_is_deterministic(hf):
+    r = Run(SMALL, n_group=8, topk_group=4, seed=8)
+    x = synth.make_x_dev(1, SMALL["hidden"], seed=8)
+    a = r.forward(x)
+    b = r.forward(x)
+    assert np.array_equal(a["out"].view(np.uint32), b["out"].view(np.uint32))
+    x.free()
+    r.free()
+
+
+def test_host_contract_moe_layer(hf):
+    # hfmoe_moe_layer: host float[hidden] in and out, as GLMForward::moeLayer.
+    r = Run(SMALL, seed=13)
+    xh = O.make_x(1, SMALL["hidden"], 13)[0].copy()
+    out = np.zeros(SMALL["hidden"], np.float32)
+    capi.call("hfmoe_moe_layer", 0, xh.ctypes.data, out.ctypes.data)
+    ref, lg, idx, w = r.ref.forward(xh)
+    assert_close(out, ref, "host contract")
+    r.free()
+
+
+def test_multi_token_small(hf):
+    T = 4
+    r = Run(SMALL, n_group=8, topk_group=4, seed=17, T=T)
+    x = synth.make_x_dev(T, SMALL["hidden"], seed=17)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * SMALL["hidden"]).reshape(T, -1)
+    for t in range(T):
+        r.check_token(xh[t], res, t)
+    x.free()
+    r.free()
+
+
+def test_unregistered_layer_and_bad_T_fail(hf):
+    r = Run(SMALL, seed=1, T=2)
+    x = synth.make_x_dev(2, SMALL["hidden"], seed=1)
+    out = capi.DeviceBuffer(2 * SMALL["hidden"] * 4)
+    L = capi.load()
+    assert L.hfmoe_moe_forward(7, x.ptr, 1, out.ptr, None) == capi.ERR_NOT_REGISTERED
+    assert L.hfmoe_moe_forward(0, x.ptr, 3, out.ptr, None) == capi.ERR_INVALID_ARGUMENT
+    assert L.hfmoe_moe_forward(0, x.ptr, 0, out.ptr, None) == capi.OK
+    x.free()
+    out.free()
+    r.free()
+
+
+def test_expert_cache_stage_and_ffn(hf):
+    # gpuExpertStage / gpuExpertFFN contract (cuda_backend.h:72-85).
+    d, I = 2048, 1024
+    rng_w = O.fill_bf16(3 * d * I, 31, 1, 0.0, 0.02)
+    x = O.fill_f32(d, 32, 2, 0.0, 1.0)
+    capi.call("hfmoe_expert_cache_config", 2, 2)
+    assert capi.load().hfmoe_experts_enabled() == 1
+    capi.call("hfmoe_expert_stage", 1, 3, rng_w.ctypes.data, d, I)
+    out = np.zeros(d, np.float32)
+    capi.call("hfmoe_expert_ffn", 1, 3, x.ctypes.data, out.ctypes.data, d, I)
+    scratch = np.zeros(3 * I, np.float32)
+    ref = np.zeros(d, np.float32)
+    g = rng_w[: d * I]
+    u = rng_w[d * I: 2 * d * I]
+    dn = rng_w[2 * d * I:]
+    O.lib().orc_expert_ffn(g.ctypes.data, u.ctypes.data, dn.ctypes.data, x.ctypes.data, ref.ctypes.data,
+                           d, I, scratch.ctypes.data)
+    assert_close(out, ref, "expert ffn")
+    # Not resident -> error, as gpuExpertFFN returns false.
+    assert capi.load().hfmoe_expert_ffn(1, 4, x.ctypes.data, out.ctypes.data, d, I) == capi.ERR_NOT_REGISTERED
+    capi.load().hfmoe_expert_cache_shutdown()
+
+
+def test_self_test_passes(hf):
+    capi.call("hfmoe_self_test")
+
+
+def test_streamed_experts_small(hf):
+    # Routed experts in pinned host RAM; only selected ones cross PCIe.
+    r = Run(SMALL, n_group=8, topk_group=4, seed=23, on_host=True)
+    for tok in range(3):
+        x = synth.make_x_dev(1, SMALL["hidden"], seed=100 + tok)
+        res = r.forward(x)
+        xh = x.download(np.float32, SMALL["hidden"])
+        r.check_token(xh, res, 0)
+        x.free()
+    r.free()
+
+
+def test_mlp_block_chain(hf):
+    # h += MoE(RMSNorm(h)) over three chained layers (glm_forward.cpp:785-796).
+    dims = dict(hidden=1024, inter=512, n_experts=32, top_k=4)
+    shape = synth.LayerShape(n_group=4, topk_group=2, **dims)
+    capi.call("hfmoe_configure", shape.config(max_tokens=1))
+    layers = [synth.DeviceLayer(shape, layer=l, seed=40, with_norm=True, experts_on_host=(l == 1))
+              for l in range(3)]
+    refs = [O.SyntheticLayer(O.LayerSpec(n_group=4, topk_group=2, seed=40, layer=l, **dims)) for l in range(3)]
+    h = synth.make_x_dev(1, dims["hidden"], seed=41)
+    hh = h.download(np.float32, dims["hidden"])
+    for l in range(3):
+        capi.call("hfmoe_mlp_block", l, h.ptr, 1, None)
+        norm_w = O.fill_bf16(dims["hidden"], 40, O.tensor_id(l, O.ROLE_NORM), 1.0, 0.05)
+        xn = O.rmsnorm(norm_w, hh, 1e-5)
+        out, lg, idx, w = refs[l].forward(xn)
+        hh = hh + out
+    capi.call("hfmoe_synchronize")
+    got = h.download(np.float32, dims["hidden"])
+    assert_close(got, hh, "three-layer chain")
+    for L in layers:
+        L.free()
+    h.free()
