@@ -13,6 +13,7 @@
 namespace hf {
 
 State g;
+LaunchTiming g_timing;
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -30,33 +31,46 @@ int fail_hip(hipError_t e, const char* what) {
 
 hipStream_t pick_stream(void* s) { return s ? reinterpret_cast<hipStream_t>(s) : g.stream; }
 
-// ---- profiling: hipEvents recorded around each launch on its stream ----
+// ---- profiling: the next launch of a section records its own dispatch
+// timestamps into a pair of pooled events (launch() in hf_kernels.h) ----
+static hipEvent_t pooled_event() {
+    hipEvent_t e = nullptr;
+    if (!g.event_pool.empty()) {
+        e = g.event_pool.back();
+        g.event_pool.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+        e = nullptr;
+    }
+    return e;
+}
+
 void prof_begin(Pending& p, const char* name, hipStream_t s) {
+    (void)s;
     p.name = nullptr;
     if (!g.prof_on) return;
-    hipEvent_t a = nullptr, b = nullptr;
-    if (!g.event_pool.empty()) {
-        a = g.event_pool.back();
-        g.event_pool.pop_back();
-    } else if (hipEventCreate(&a) != hipSuccess) {
-        return;
-    }
-    if (!g.event_pool.empty()) {
-        b = g.event_pool.back();
-        g.event_pool.pop_back();
-    } else if (hipEventCreate(&b) != hipSuccess) {
+    hipEvent_t a = pooled_event();
+    if (!a) return;
+    hipEvent_t b = pooled_event();
+    if (!b) {
         g.event_pool.push_back(a);
         return;
     }
-    hipEventRecord(a, s);
     p.name = name;
     p.start = a;
     p.stop = b;
+    g_timing.start = a;
+    g_timing.stop = b;
 }
 
 void prof_end(Pending& p, hipStream_t s) {
+    (void)s;
     if (!p.name) return;
-    hipEventRecord(p.stop, s);
+    if (g_timing.start == p.start) {  // nothing was launched in the section
+        g_timing = LaunchTiming{};
+        g.event_pool.push_back(p.start);
+        g.event_pool.push_back(p.stop);
+        return;
+    }
     g.pending.push_back(p);
 }
 
@@ -78,7 +92,7 @@ void prof_drain() {
 
 static void free_workspace() {
     Workspace& w = g.ws;
-    void* ptrs[] = {w.logits, w.idx, w.wts, w.h, w.counter, w.x_io, w.out_io, w.tmp};
+    void* ptrs[] = {w.logits, w.scores, w.idx, w.wts, w.h, w.counter, w.x_io, w.out_io, w.tmp};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = Workspace{};
@@ -95,6 +109,7 @@ static int alloc_workspace() {
         size_t bytes;
     } list[] = {
         {(void**)&w.logits, sizeof(float) * (size_t)T * c.E},
+        {(void**)&w.scores, sizeof(float2) * (size_t)T * c.E},
         {(void**)&w.idx, sizeof(int) * (size_t)T * c.k},
         {(void**)&w.wts, sizeof(float) * (size_t)T * c.k},
         {(void**)&w.h, sizeof(float) * (size_t)nslots * c.I},

@@ -224,11 +224,8 @@ int hfmoe_expert_ffn(int layer, int expert_id, const float* x, float* out, int h
     e = hipMemcpyAsync(c.x, x, sizeof(float) * hidden, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return fail_hip(e, "H2D x");
     g.pcie_bytes += sizeof(float) * hidden;
-    Pending p;
-    prof_begin(p, "expert_ffn", s);
     e = launch_expert_ffn(d.w, d.w + half, d.w + 2 * half, c.x, c.h, c.out, hidden, inter,
-                          g.num_cus * 2, s);
-    prof_end(p, s);
+                          gu_blocks(), dn_blocks(), s);
     if (e != hipSuccess) return fail_hip(e, "expert ffn launch");
     e = hipMemcpyAsync(out, c.out, sizeof(float) * hidden, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);

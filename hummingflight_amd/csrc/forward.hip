@@ -2,11 +2,14 @@
 // glm_forward.cpp:509-661): router -> selection -> expert SwiGLU -> weighted
 // combine + shared expert, all on one stream with no host round trip.
 #include "hf_api_internal.h"
+#include "hf_select.h"
 
 namespace hf {
 
-int gu_blocks() { return env_int("HFMOE_GU_BLOCKS", g.num_cus * 2); }
-int dn_blocks() { return env_int("HFMOE_DN_BLOCKS", g.num_cus * 2); }
+// Three 4-wave blocks per CU: at d = 6144 every wavefront owns exactly 6 rows.
+int gu_blocks() { return env_int("HFMOE_GU_BLOCKS", g.num_cus * 3); }
+// One block (a band of output rows) per CU.
+int dn_blocks() { return env_int("HFMOE_DN_BLOCKS", g.num_cus); }
 
 static int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s) {
     if (!dbg) return HFMOE_OK;
@@ -37,11 +40,22 @@ int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const h
     const int nslots = c.k + c.n_shared;
     Pending p;
     prof_begin(p, "router", s);
-    hipError_t e = launch_router_t1(x, L.dev, c, g.ws.logits, g.ws.idx, g.ws.wts, g.ws.counter, s);
+    hipError_t e = launch_router_logits_t1(x, L.dev, c, g.ws.logits, g.ws.scores, s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "router launch");
+    // The gate/up kernel routes in place, overlapped with the loads of the
+    // shared expert's first rows (HFMOE_FUSE_SELECT=0 runs selection as its own
+    // kernel first, for comparison).
+    const bool fused = env_int("HFMOE_FUSE_SELECT", 1) != 0;
+    if (!fused) {
+        prof_begin(p, "select", s);
+        e = launch_select(g.ws.scores, 1, c, g.ws.idx, g.ws.wts, s);
+        prof_end(p, s);
+        if (e != hipSuccess) return fail_hip(e, "select launch");
+    }
     prof_begin(p, "expert_gateup", s);
-    e = launch_gateup_t1(x, L.dev, c, g.ws.idx, g.ws.h, nslots, gu_blocks(), s);
+    e = launch_gateup_t1(x, L.dev, c, fused ? g.ws.scores : nullptr, g.ws.idx, g.ws.wts, g.ws.h,
+                         nslots, gu_blocks(), s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "gate/up launch");
     prof_begin(p, "expert_down", s);
@@ -63,13 +77,17 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     const Cfg& c = g.cfg;
     const int nslots = c.k + c.n_shared;
     Pending p;
-    prof_begin(p, "router_tokens", s);
-    hipError_t e = launch_router_tokens(x, T, L.dev, c, g.ws.logits, g.ws.idx, g.ws.wts, s);
+    prof_begin(p, "router", s);
+    hipError_t e = launch_router_logits(x, T, L.dev, c, g.ws.logits, g.ws.scores, s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "router launch");
+    prof_begin(p, "select", s);
+    e = launch_select(g.ws.scores, T, c, g.ws.idx, g.ws.wts, s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "select launch");
     for (int t = 0; t < T; ++t) {
-        e = launch_gateup_t1(x + (size_t)t * c.d, L.dev, c, g.ws.idx + (size_t)t * c.k, g.ws.h,
-                             nslots, gu_blocks(), s);
+        e = launch_gateup_t1(x + (size_t)t * c.d, L.dev, c, nullptr, g.ws.idx + (size_t)t * c.k,
+                             nullptr, g.ws.h, nslots, gu_blocks(), s);
         if (e != hipSuccess) return fail_hip(e, "gate/up launch");
         e = launch_down_t1(g.ws.h, L.dev, c, g.ws.idx + (size_t)t * c.k, g.ws.wts + (size_t)t * c.k,
                            nullptr, out + (size_t)t * c.d, nslots, dn_blocks(), s);

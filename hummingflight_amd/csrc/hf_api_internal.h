@@ -15,6 +15,7 @@ namespace hf {
 
 struct Workspace {
     float* logits = nullptr;     // [maxT, E]
+    float2* scores = nullptr;    // [maxT, E] (sigmoid, sigmoid + bias)
     int* idx = nullptr;          // [maxT, k]
     float* wts = nullptr;        // [maxT, k]
     float* h = nullptr;          // [k + n_shared, I]  (T = 1 path)

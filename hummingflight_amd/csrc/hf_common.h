@@ -33,6 +33,8 @@ struct LayerDev {
 };
 
 constexpr int kMaxTopK = 8;
+constexpr int kMaxGroups = 64;
+constexpr int kMaxExperts = 1024;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -58,23 +60,71 @@ __device__ __forceinline__ float dot8(const u32x4 w, const float* x, float acc) 
     return acc;
 }
 
+// ---- cross-lane steps on the DPP network (GFX9 encodings) ----
+// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_ror:4 = 0x124,
+// row_ror:8 = 0x128, row_mirror = 0x140, row_half_mirror = 0x141.
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the 64 lanes; every lane gets the same value (fixed order: rows by
+// DPP butterfly, then (row0 + row1) + (row2 + row3)).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f<kDppQuadXor1>(v);
+    v += dpp_f<kDppQuadXor2>(v);
+    v += dpp_f<kDppRowRor4>(v);
+    v += dpp_f<kDppRowRor8>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+    const float v2 = dpp_f<CTRL>(v);
+    const int i2 = dpp_i<CTRL>(i);
+    if (ranks_before(v2, i2, v, i)) {
+        v = v2;
+        i = i2;
+    }
 }
 
 // Wave-wide argmax over (value desc, index asc); every lane gets the winner.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
+    argmax_step<kDppQuadXor1>(v, i);
+    argmax_step<kDppQuadXor2>(v, i);
+    argmax_step<kDppRowRor4>(v, i);
+    argmax_step<kDppRowRor8>(v, i);
+    float bv = readlane_f(v, 0);
+    int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v2 = __shfl_xor(v, o, 64);
-        const int i2 = __shfl_xor(i, o, 64);
-        if (v2 > v || (v2 == v && i2 < i)) {
-            v = v2;
-            i = i2;
+    for (int r = 16; r < 64; r += 16) {
+        const float rv = readlane_f(v, r);
+        const int ri = __builtin_amdgcn_readlane(i, r);
+        if (ranks_before(rv, ri, bv, bi)) {
+            bv = rv;
+            bi = ri;
         }
     }
+    v = bv;
+    i = bi;
 }
 
 // Weight loads that stream through the cache hierarchy once.

@@ -1,25 +1,67 @@
 // hf_kernels.h -- launchers of the MoE-block kernels (host side).
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "hf_common.h"
 
 namespace hf {
 
-constexpr int kMaxExperts = 1024;   // selection keeps ceil(E/64) scores per lane
+// Timing hook: when set, the next launch records its own dispatch start and
+// end timestamps into these events (hipExtLaunchKernelGGL) and clears the hook,
+// so a measured duration is the kernel's alone, with no extra packets queued.
+struct LaunchTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+extern LaunchTiming g_timing;
+
+template <typename... Params>
+inline hipError_t launch_exact(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem,
+                               hipStream_t s, Params... args) {
+    if (g_timing.start) {
+        const LaunchTiming t = g_timing;
+        g_timing = LaunchTiming{};
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, t.start, t.stop, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+    }
+    return hipGetLastError();
+}
+
+// Launch with every argument converted to the kernel's exact parameter type
+// (the extended launch packs arguments by their own types).
+template <typename... Params, typename... Args>
+inline hipError_t launch(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem,
+                         hipStream_t s, Args... args) {
+    static_assert(sizeof...(Params) == sizeof...(Args), "kernel argument count");
+    return launch_exact<Params...>(kernel, grid, block, shmem, s, static_cast<Params>(args)...);
+}
+
 constexpr int kRouterTokTile = 8;   // tokens per pass of the multi-token router GEMV
 constexpr int kMaxSlots = 16;       // routed + shared slices handled by the T=1 GEMVs
+constexpr int kDownMaxRows = 64;    // output rows per block of the decode down projection
 
 // router.hip
-hipError_t launch_router_t1(const float* x, const LayerDev& L, const Cfg& c, float* logits,
-                            int* sel_idx, float* sel_w, unsigned int* counter, hipStream_t s);
-hipError_t launch_router_tokens(const float* x, int T, const LayerDev& L, const Cfg& c,
-                                float* logits, int* sel_idx, float* sel_w, hipStream_t s);
+// Logits [E] of one token (x FP32 [d]) and score pairs (sigmoid, sigmoid + bias).
+hipError_t launch_router_logits_t1(const float* x, const LayerDev& L, const Cfg& c, float* logits,
+                                   float2* scores, hipStream_t s);
+// Logits and score pairs [T, E] of T tokens.
+hipError_t launch_router_logits(const float* x, int T, const LayerDev& L, const Cfg& c,
+                                float* logits, float2* scores, hipStream_t s);
+// (Group-limited) top-k + normalise + scale from score pairs, one wave per
+// token: sel_idx/sel_w [T, k].
+hipError_t launch_select(const float2* scores, int T, const Cfg& c, int* sel_idx, float* sel_w,
+                         hipStream_t s);
 
 // expert_gemv.hip -- decode (T = 1) expert SwiGLU.
 // Slots 0..k-1 are the selected experts (sel_idx), slots k.. are the shared
 // expert's n_shared slices of I rows.  h: FP32 [nslots, I].
-hipError_t launch_gateup_t1(const float* x, const LayerDev& L, const Cfg& c, const int* sel_idx,
-                            float* h, int nslots, int blocks, hipStream_t s);
+// With `scores` (E <= 256) the kernel routes in place and writes sel_idx/sel_w;
+// without, sel_idx holds the k routed ids on entry.
+hipError_t launch_gateup_t1(const float* x, const LayerDev& L, const Cfg& c, const float2* scores,
+                            int* sel_idx, float* sel_w, float* h, int nslots, int blocks,
+                            hipStream_t s);
 // out[j] = sum_s weight_s * (Wd_s[j,:] . h_s) (+ addend[j] when addend is not null);
 // weight = sel_w for routed slots, 1 for shared slices.
 hipError_t launch_down_t1(const float* h, const LayerDev& L, const Cfg& c, const int* sel_idx,
@@ -29,8 +71,8 @@ hipError_t launch_down_t1(const float* h, const LayerDev& L, const Cfg& c, const
 // Single-expert FFN on explicit device weights (the per-expert boundary of
 // gpuExpertFFN, cuda_backend.h:79-85): out = Wd.(silu(Wg.x) * (Wu.x)).
 hipError_t launch_expert_ffn(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd,
-                             const float* x, float* h, float* out, int d, int I, int blocks,
-                             hipStream_t s);
+                             const float* x, float* h, float* out, int d, int I, int gu_blocks,
+                             int dn_blocks, hipStream_t s);
 
 // rng.hip -- seeded synthetic tensors (same bits as the generator the tests use).
 hipError_t launch_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t tensor,

@@ -31,15 +31,13 @@ __global__ void add_inplace_kernel(float* __restrict__ dst, const float* __restr
 
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, s, h, w, out, d, eps);
-    return hipGetLastError();
+    return launch(rmsnorm_kernel, dim3(T), dim3(256), 0, s, h, w, out, d, eps);
 }
 
 hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s) {
     size_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(add_inplace_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, src, n);
-    return hipGetLastError();
+    return launch(add_inplace_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, src, n);
 }
 
 }  // namespace hf

@@ -66,17 +66,15 @@ static unsigned fill_blocks(uint64_t n) {
 hipError_t launch_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t tensor,
                                    uint64_t first, float mean, float stdev, hipStream_t s) {
     const uint64_t key = host_sm64(seed ^ host_sm64(tensor));
-    hipLaunchKernelGGL(fill_bf16_kernel, dim3(fill_blocks(n)), dim3(256), 0, s, out, n, key,
+    return launch(fill_bf16_kernel, dim3(fill_blocks(n)), dim3(256), 0, s, out, n, key,
                        first, mean, stdev);
-    return hipGetLastError();
 }
 
 hipError_t launch_fill_normal_f32(float* out, uint64_t n, uint64_t seed, uint64_t tensor,
                                   uint64_t first, float mean, float stdev, hipStream_t s) {
     const uint64_t key = host_sm64(seed ^ host_sm64(tensor));
-    hipLaunchKernelGGL(fill_f32_kernel, dim3(fill_blocks(n)), dim3(256), 0, s, out, n, key, first,
+    return launch(fill_f32_kernel, dim3(fill_blocks(n)), dim3(256), 0, s, out, n, key, first,
                        mean, stdev);
-    return hipGetLastError();
 }
 
 }  // namespace hf

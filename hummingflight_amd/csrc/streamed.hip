@@ -89,9 +89,13 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
 
     Pending p;
     prof_begin(p, "router", s);
-    hipError_t e = launch_router_t1(x, L.dev, c, g.ws.logits, g.ws.idx, g.ws.wts, g.ws.counter, s);
+    hipError_t e = launch_router_logits_t1(x, L.dev, c, g.ws.logits, g.ws.scores, s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "router launch");
+    prof_begin(p, "select", s);
+    e = launch_select(g.ws.scores, 1, c, g.ws.idx, g.ws.wts, s);
+    prof_end(p, s);
+    if (e != hipSuccess) return fail_hip(e, "select launch");
     e = hipMemcpyAsync(P.idx_host, g.ws.idx, sizeof(int) * c.k, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipEventRecord(P.routed, s);
     if (e != hipSuccess) return fail_hip(e, "routing readback");
@@ -103,7 +107,7 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
         cs.k = 0;
         float* hs = g.ws.h + (size_t)c.k * c.I;
         prof_begin(p, "shared_gateup", s);
-        e = launch_gateup_t1(x, L.dev, cs, nullptr, hs, c.n_shared, gu_blocks(), s);
+        e = launch_gateup_t1(x, L.dev, cs, nullptr, nullptr, nullptr, hs, c.n_shared, gu_blocks(), s);
         prof_end(p, s);
         if (e != hipSuccess) return fail_hip(e, "shared gate/up launch");
         prof_begin(p, "shared_down", s);
@@ -172,7 +176,7 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
     LayerDev Lr = L.dev;
     Lr.etab = P.etab_dev;
     prof_begin(p, "expert_gateup", s);
-    e = launch_gateup_t1(x, Lr, cr, P.iota_dev, g.ws.h, c.k, gu_blocks(), s);
+    e = launch_gateup_t1(x, Lr, cr, nullptr, P.iota_dev, nullptr, g.ws.h, c.k, gu_blocks(), s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "routed gate/up launch");
     prof_begin(p, "expert_down", s);
