@@ -138,7 +138,7 @@ def run_decode(args) -> dict:
                    "weights": "HBM-resident BF16 ~N(0,0.02)"},
         "roofline": {"bound": "hbm", "kernel": "expert_gateup", "achieved": round(dom["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": traffic_from_profile("expert_gateup")},
         "layer_hbm": {"algorithmic_bytes": algo["layer"], "achieved_gbs": round(layer_gbs, 1),
                       "frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "ms_per_step_with_kernel_events": sec_prof * 1e3,
@@ -152,12 +152,42 @@ def run_decode(args) -> dict:
     return res
 
 
+def run_copy(args) -> None:
+    """Counter calibration: 4 GiB device-to-device copies (HIP's own copy kernel)."""
+    n = 4 << 30
+    a = capi.DeviceBuffer(n)
+    b = capi.DeviceBuffer(n)
+    capi.call("hfmoe_memset", a.ptr, 1, n)
+    t0 = time.perf_counter()
+    for _ in range(max(args.steps, 1)):
+        capi.call("hfmoe_memcpy_d2d", b.ptr, a.ptr, n)
+    dt = (time.perf_counter() - t0) / max(args.steps, 1)
+    print(json.dumps({"workload": "copy_calibration", "bytes_read_per_copy": n, "bytes_written_per_copy": n,
+                      "copies": args.steps, "gbs_read_plus_write": round(2 * n / dt / 1e9, 1)}), flush=True)
+    a.free()
+    b.free()
+
+
+def traffic_from_profile(kernel: str) -> int | None:
+    """HBM bytes per launch of `kernel` from the committed counter summary."""
+    path = os.path.join(ROOT, "profiles", "decode_t1_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            for item in line.split(":", 1)[1].split():
+                name, _, val = item.partition("=")
+                if name == kernel:
+                    return int(val)
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -167,6 +197,10 @@ def main() -> int:
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
     capi.call("hfmoe_init", 0)
+    if args.workload == "copy":
+        run_copy(args)
+        capi.load().hfmoe_shutdown()
+        return 0
     res = run_decode(args)
     line = {"metric": METRIC, "value": round(res.pop("value"), 2), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res.pop("ms_per_step"), 5),
