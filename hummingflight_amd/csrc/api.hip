@@ -194,6 +194,7 @@ void hfmoe_shutdown(void) {
         if (kv.second.etab_dev) hipFree(kv.second.etab_dev);
     g.layers.clear();
     free_workspace();
+    grouped_workspace_free();
     prof_drain();
     for (auto ev : g.event_pool) hipEventDestroy(ev);
     g.event_pool.clear();

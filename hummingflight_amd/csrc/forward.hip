@@ -11,7 +11,7 @@ int gu_blocks() { return env_int("HFMOE_GU_BLOCKS", g.num_cus * 3); }
 // One block (a band of output rows) per CU.
 int dn_blocks() { return env_int("HFMOE_DN_BLOCKS", g.num_cus); }
 
-static int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s) {
+int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s) {
     if (!dbg) return HFMOE_OK;
     const Cfg& c = g.cfg;
     hipError_t e = hipSuccess;
@@ -69,11 +69,11 @@ int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const h
 
 namespace hf {
 
-// Multi-token forward, token by token over the decode kernels.  Every token
-// re-streams its experts' weights, so this is the correctness path for small T
-// until the dispatch + grouped kernels take over.
-int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
-                    const hfmoe_route_debug* dbg) {
+// Multi-token forward, token by token over the decode kernels (every token
+// re-streams its experts' weights): used for shapes the grouped GEMM does not
+// tile (hidden or intermediate not a multiple of 32).
+int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                      const hfmoe_route_debug* dbg) {
     const Cfg& c = g.cfg;
     const int nslots = c.k + c.n_shared;
     Pending p;
@@ -95,8 +95,5 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     }
     return copy_debug(dbg, T, s);
 }
-
-int grouped_workspace_alloc() { return HFMOE_OK; }
-void grouped_workspace_free() {}
 
 }  // namespace hf

@@ -1,6 +1,7 @@
 // hf_api_internal.h -- library state shared by the C-ABI translation units.
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 #include <map>
 #include <string>
@@ -29,20 +30,22 @@ struct Workspace {
 struct GroupedWorkspace {
     int* counts = nullptr;       // [E]
     int* offsets = nullptr;      // [E + 1]
-    int* perm = nullptr;         // [maxT*k]
-    int* tile_info = nullptr;    // scheduling scratch
-    uint16_t* xb = nullptr;      // [maxT*k, d] x gathered in expert order, BF16 hi
-    uint16_t* xl = nullptr;      // [maxT*k, d] BF16 lo residual
-    uint16_t* hb = nullptr;      // [maxT*k, I] h hi
+    int* perm = nullptr;         // [maxT*k] pair ids in (expert, pair) order
+    int* row_token = nullptr;    // [maxT*k] token of each sorted row
+    int* tile_expert = nullptr;  // [max_tiles] expert of each 128-row M tile
+    int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
+    int* ntiles = nullptr;       // [1] M tiles in use
+    unsigned int* lo_flag = nullptr;  // [1] x has a nonzero BF16 lo half
+    uint16_t* xh = nullptr;      // [maxT, d] x BF16 hi (token order)
+    uint16_t* xl = nullptr;      // [maxT, d] x BF16 lo
+    uint16_t* hh = nullptr;      // [maxT*k, I] h hi (sorted rows)
     uint16_t* hl = nullptr;      // [maxT*k, I] h lo
-    float* y = nullptr;          // [maxT*k, d] per-pair expert outputs
-    uint16_t* sxb = nullptr;     // shared expert: x BF16 hi/lo in token order
-    uint16_t* sxl = nullptr;
-    uint16_t* shb = nullptr;     // shared h hi/lo [maxT, S*I]
+    float* y = nullptr;          // [maxT*k, d] per-pair expert outputs at pair slots
+    uint16_t* shh = nullptr;     // [maxT, S*I] shared-expert h hi / lo
     uint16_t* shl = nullptr;
-    float* sy = nullptr;         // shared output [maxT, d]
-    unsigned int* flags = nullptr;
-    size_t bytes = 0;
+    float* part = nullptr;       // [ksplit, maxT, E] router split-K partials
+    int max_tiles = 0;
+    int ksplit = 1;
 };
 
 struct LayerState {
@@ -124,6 +127,10 @@ int dn_blocks();
 int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg);
 int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                     const hfmoe_route_debug* dbg);
+int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                      const hfmoe_route_debug* dbg);
+int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s);
+// grouped_forward.hip
 int grouped_workspace_alloc();
 void grouped_workspace_free();
 // streamed.hip

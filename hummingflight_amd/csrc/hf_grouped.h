@@ -1,0 +1,57 @@
+// hf_grouped.h -- multi-token MoE: dispatch and the BF16 MFMA grouped GEMM.
+#pragma once
+
+#include "hf_common.h"
+
+namespace hf {
+
+constexpr int kGemmTileRows = 128;  // M rows per grouped-GEMM tile
+
+enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2, EPI_COMBINE = 3 };
+
+// Arguments of one grouped GEMM launch (see grouped_gemm.hip).
+struct GemmArgs {
+    int K;                      // reduction length (multiple of 32 * ksplit)
+    int N;                      // output columns (SWIGLU: intermediate rows per matrix)
+    int n_tiles;                // ceil(N / columns per tile)
+    // M tiling: tile i covers rows [tile_row0[i], min(+128, group_end[tile_group[i]]))
+    const int* tile_group;      // null: one group, rows [0, rows_total) in 128-row tiles
+    const int* tile_row0;
+    const int* ntiles_dev;      // device count of M tiles (null: m_tiles)
+    int m_tiles;
+    const int* group_end;       // rows of group g end at group_end[g] (null: rows_total)
+    int rows_total;
+    // A: BF16 rows of length K; row r reads row a_rowmap[r] (or r) of a_hi / a_lo
+    const uint16_t* a_hi;
+    const uint16_t* a_lo;       // null: no lo half
+    const unsigned* a_lo_flag;  // device flag: lo half present (null: use a_lo when given)
+    const int* a_rowmap;
+    // B: [N, K] rows of group g at b_tab[3g + b_which] (and +1: up for SWIGLU), else fixed
+    const uint16_t* const* b_tab;
+    int b_which;
+    const uint16_t* b_fixed0;
+    const uint16_t* b_fixed1;
+    int b_ld;                   // B row stride in elements
+    // epilogue operands
+    float* out_f32;             // PARTIAL [ksplit][rows][N]; SCATTER y rows; COMBINE out [T][N]
+    uint16_t* h_hi;             // SWIGLU h [rows][N] hi / lo
+    uint16_t* h_lo;
+    const int* scatter_rows;    // SCATTER: y row of GEMM row r
+    const float* comb_w;        // COMBINE: weights [T][comb_k]
+    const float* comb_y;        // COMBINE: y [T * comb_k][N]
+    int comb_k;
+    int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
+};
+
+hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s);
+hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
+                             hipStream_t s);
+hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, const float* bias,
+                                float* logits, float2* scores, hipStream_t s);
+// Stable counting sort of the T*k (token, rank) pairs by expert plus the M-tile
+// list (tile_rows rows per tile) of the grouped GEMM.
+hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int* counts,
+                           int* offsets, int* perm, int* row_token, int* tile_expert,
+                           int* tile_row0, int* ntiles, hipStream_t s);
+
+}  // namespace hf
