@@ -1,16 +1,24 @@
 """MoE-block benchmark on one MI355X.
 
-Default workload: the full-shape MoE layer at decode, T=1 token (d=6144,
-256 routed experts + 1 shared, SwiGLU I=2048, router 8 groups keep 4, top-8,
-weights BF16 ~N(0,0.02) resident in HBM).  One step = one MoE-layer forward
-over one token; inputs are already in HBM when the timed region starts.
+Default workload (`decode`): the full-shape MoE layer at decode, T=1 token
+(d=6144, 256 routed experts + 1 shared, SwiGLU I=2048, router 8 groups keep 4,
+top-8, weights BF16 ~N(0,0.02) resident in HBM).  One step = one MoE-layer
+forward over one token; inputs are already in HBM when the timed region starts.
 
-Prints one JSON line: tokens/s as `value`, the dominant kernel's achieved HBM
-bandwidth against the 8 TB/s peak as `roofline` (durations from hipEvents the
-library records on its launch stream during the timed steps), and the
-reference CPU path timed on this host as `cpu_baseline`.
+Other workloads of the same layer:
+  batched   T=64 tokens, correction bias calibrated for Zipf(1.1) expert
+            popularity (tests/golden/zipf_bias_e256.json); HBM-bound
+  prefill   T=4096 tokens, near-uniform routing (bias ~N(0,0.001)); MFMA-bound
+  streamed  8 chained layers (RMSNorm + MoE + residual), T=1, routed experts in
+            pinned host RAM, the selected ones copied to HBM on a side stream
+  copy      counter calibration (4 GiB device-to-device copies)
 
-    python bench.py [--steps K] [--warmup W] [--workload decode|batched|prefill|streamed]
+Prints one JSON line: tokens/s as `value`, the dominant kernel's achieved rate
+against its roofline as `roofline` (durations from the kernels' own dispatch
+timestamps, recorded on the launch stream during a second pass of the timed
+steps), and the reference CPU path timed on this host as `cpu_baseline`.
+
+    python bench.py [--steps K] [--warmup W] [--workload decode|batched|prefill|streamed|copy]
 """
 from __future__ import annotations
 
@@ -113,12 +121,8 @@ def run_decode(args) -> dict:
             capi.check(rc)
 
     sec = time_steps(step, args.steps, args.warmup)
-    # Same steps again with per-kernel hipEvents on the launch stream.
-    capi.call("hfmoe_profile_reset")
-    capi.call("hfmoe_profile_enable", 1)
-    sec_prof = time_steps(step, args.steps, 0)
-    capi.call("hfmoe_profile_enable", 0)
-    prof = capi.profile_read()
+    # Same steps again, each kernel recording its own dispatch timestamps.
+    prof, sec_prof = profiled_pass(step, args.steps)
     algo = algorithmic_bytes_t1(shape)
     kernels = {}
     for name, (n, ms) in prof.items():
@@ -152,6 +156,195 @@ def run_decode(args) -> dict:
     return res
 
 
+def grouped_algorithmic(shape: synth.LayerShape, T: int, U: int) -> dict[str, tuple[int, int]]:
+    """(bytes, flops) each multi-token kernel must move / compute at least once.
+
+    U = distinct routed experts hit by the batch; the shared expert is one more
+    group in the same GEMM launches.  Weights are read once per launch,
+    activations once per token (x as BF16 [T, d]), the SwiGLU intermediate
+    counted at 4 bytes per element, expert outputs as FP32.
+    """
+    d, I, E, k, S = shape.hidden, shape.inter, shape.n_experts, shape.top_k, shape.n_shared
+    R = T * k + S * T  # GEMM rows: routed (token, rank) pairs + shared-expert rows
+    return {
+        "router_gemm": (E * d * 2 + T * d * 2 + T * E * 4, 2 * T * E * d),
+        "expert_gateup_gemm": ((U + S) * 2 * I * d * 2 + T * d * 2 + R * I * 4, 2 * R * 2 * I * d),
+        "expert_down_gemm": ((U + S) * d * I * 2 + R * I * 4 + R * d * 4, 2 * R * d * I),
+        "combine": (R * d * 4 + T * k * 4 + T * d * 4, 2 * T * k * d),
+    }
+
+
+def kernel_table(prof: dict, algo: dict) -> dict:
+    kernels = {}
+    for name, (n, ms) in prof.items():
+        avg_us = ms * 1e3 / max(n, 1)
+        row = {"launches": n, "avg_us": round(avg_us, 3)}
+        if name in algo:
+            nbytes, flops = algo[name]
+            row.update(algorithmic_bytes=nbytes, gbs=round(nbytes / (avg_us * 1e-6) / 1e9, 1),
+                       algorithmic_flops=flops, tflops=round(flops / (avg_us * 1e-6) / 1e12, 2))
+        kernels[name] = row
+    return kernels
+
+
+def profiled_pass(step, steps: int) -> tuple[dict, float]:
+    capi.call("hfmoe_profile_reset")
+    capi.call("hfmoe_profile_enable", 1)
+    sec = time_steps(step, steps, 0)
+    capi.call("hfmoe_profile_enable", 0)
+    return capi.profile_read(), sec
+
+
+def run_grouped(args, workload: str) -> dict:
+    """Batched decode (T=64, Zipf routing) or a prefill chunk (T=4096)."""
+    shape = synth.LayerShape(**FULL)
+    if workload == "batched":
+        T = 64
+        with open(os.path.join(ROOT, "tests", "golden", "zipf_bias_e256.json")) as fh:
+            zb = json.load(fh)
+        seed = zb["layer_seed"]  # the bias is calibrated for this layer's router
+        layer_kw = dict(bias=np.array(zb["bias"], np.float32))
+        routing = "correction bias calibrated for Zipf(1.1) expert popularity"
+    else:
+        T = 4096
+        seed = args.seed
+        layer_kw = dict(bias_std=0.001)
+        routing = "near-uniform, correction bias ~N(0,0.001)"
+    capi.call("hfmoe_configure", shape.config(max_tokens=T))
+    layer = synth.DeviceLayer(shape, layer=0, seed=seed, **layer_kw)
+    x = synth.make_x_dev(T, shape.hidden, seed=seed)
+    out = capi.DeviceBuffer(T * shape.hidden * 4)
+    idx = capi.DeviceBuffer(T * shape.top_k * 4)
+    dbg = capi.RouteDebug(None, idx.ptr, None, None, None)
+    capi.call("hfmoe_moe_forward_debug", 0, x.ptr, T, out.ptr, None, C.byref(dbg))
+    capi.call("hfmoe_synchronize")
+    counts = np.bincount(idx.download(np.int32, T * shape.top_k), minlength=shape.n_experts)
+    U = int((counts > 0).sum())
+    fwd = capi.load().hfmoe_moe_forward
+
+    def step():
+        rc = fwd(0, x.ptr, T, out.ptr, None)
+        if rc:
+            capi.check(rc)
+
+    sec = time_steps(step, args.steps, args.warmup)
+    prof, sec_prof = profiled_pass(step, args.steps)
+    algo = grouped_algorithmic(shape, T, U)
+    kernels = kernel_table(prof, algo)
+    d, I, E, S = shape.hidden, shape.inter, shape.n_experts, shape.n_shared
+    layer_bytes = (U + S) * 3 * I * d * 2 + E * d * 2 + E * 4 + 2 * T * d * 4
+    layer_flops = sum(f for _, f in algo.values())
+    if workload == "batched":
+        dom_name = max((n for n in algo if n in kernels), key=lambda n: kernels[n]["avg_us"])
+        dom = kernels[dom_name]
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": dom["gbs"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profile(dom_name, "batched_t64_hbm_traffic.md")}
+    else:
+        dom_name = "expert_gateup_gemm"
+        dom = kernels[dom_name]
+        roof = {"bound": "mfma", "kernel": dom_name, "achieved": dom["tflops"],
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": traffic_from_profile(dom_name, "prefill_t4096_hbm_traffic.md")}
+    res = {
+        "value": T / sec,
+        "ms_per_step": sec * 1e3,
+        "config": {"workload": f"moe_layer_{workload}", "tokens": T, "hidden": d, "moe_intermediate": I,
+                   "routed_experts": E, "shared_experts": S, "top_k": shape.top_k,
+                   "n_group": shape.n_group, "topk_group": shape.topk_group, "routing": routing,
+                   "distinct_experts_hit": U, "max_rows_per_expert": int(counts.max()),
+                   "weights": "HBM-resident BF16 ~N(0,0.02)"},
+        "roofline": roof,
+        "layer": {"algorithmic_bytes": layer_bytes, "achieved_gbs": round(layer_bytes / sec / 1e9, 1),
+                  "hbm_frac": round(layer_bytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+                  "algorithmic_flops": layer_flops, "achieved_tflops": round(layer_flops / sec / 1e12, 2),
+                  "mfma_frac": round(layer_flops / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "ms_per_step_with_kernel_events": sec_prof * 1e3,
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline_decode(shape, seed, args.cpu_seconds)
+        cb["sample"] += "; the reference runs a batch token by token (glm_forward.cpp:755), so its rate is per token"
+        res["cpu_baseline"] = cb
+    for b in (x, out, idx):
+        b.free()
+    layer.free()
+    return res
+
+
+def run_streamed(args) -> dict:
+    """8 chained layers, routed experts in pinned host RAM, T=1 per step."""
+    shape = synth.LayerShape(**FULL)
+    n_layers = 8
+    capi.call("hfmoe_configure", shape.config(max_tokens=1))
+    layers = [synth.DeviceLayer(shape, layer=l, seed=args.seed, experts_on_host=True, with_norm=True,
+                                distinct_experts=args.distinct_experts) for l in range(n_layers)]
+    d = shape.hidden
+    ntok = args.warmup + 2 * args.steps
+    h = synth.make_x_dev(ntok, d, seed=args.seed)
+    blk = capi.load().hfmoe_mlp_block
+    cursor = [0]
+
+    def step():
+        ptr = h.ptr + cursor[0] * d * 4
+        cursor[0] += 1
+        for l in range(n_layers):
+            rc = blk(l, ptr, 1, None)
+            if rc:
+                capi.check(rc)
+
+    for _ in range(args.warmup):
+        step()
+    capi.call("hfmoe_synchronize")
+    p0, a0 = C.c_uint64(), C.c_uint64()
+    capi.call("hfmoe_stats", C.byref(p0), C.byref(a0))
+    sec = time_steps(step, args.steps, 0)
+    p1, a1 = C.c_uint64(), C.c_uint64()
+    capi.call("hfmoe_stats", C.byref(p1), C.byref(a1))
+    prof, sec_prof = profiled_pass(step, args.steps)
+    pcie = (p1.value - p0.value) / args.steps
+    # Pinned host -> HBM copy rate of one layer's 8 selected experts, for the bound.
+    nbytes = shape.top_k * shape.expert_bytes()
+    src = capi.PinnedBuffer(nbytes)
+    dst = capi.DeviceBuffer(nbytes)
+    capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    h2d_gbs = 5 * nbytes / (time.perf_counter() - t0) / 1e9
+    achieved = pcie / sec / 1e9
+    res = {
+        "value": 1.0 / sec,
+        "ms_per_step": sec * 1e3,
+        "config": {"workload": "moe_streamed_chain", "tokens": 1, "layers": n_layers, "hidden": d,
+                   "moe_intermediate": shape.inter, "routed_experts": shape.n_experts,
+                   "shared_experts": shape.n_shared, "top_k": shape.top_k, "n_group": shape.n_group,
+                   "topk_group": shape.topk_group,
+                   "weights": f"routed experts in pinned host RAM ({args.distinct_experts} distinct weight "
+                              f"sets per layer, every expert its own cache key); routers, shared experts "
+                              f"and norms in HBM"},
+        "roofline": {"bound": "pcie", "kernel": "hipMemcpyAsync host->device", "achieved": round(achieved, 1),
+                     "peak": round(h2d_gbs, 1), "unit": "GB/s", "frac": round(achieved / h2d_gbs, 4),
+                     "traffic": int(pcie), "peak_source": "measured pinned copy of 8 experts"},
+        "pcie_bytes_per_token": int(pcie),
+        "ms_per_step_with_kernel_events": sec_prof * 1e3,
+        "kernels": kernel_table(prof, {}),
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline_decode(shape, args.seed, args.cpu_seconds)
+        cb["value"] /= n_layers
+        cb["unit"] = "tokens/s"
+        cb["sample"] += f"; one layer timed, a token crosses {n_layers} layers"
+        res["cpu_baseline"] = cb
+    src.free()
+    dst.free()
+    h.free()
+    for L in layers:
+        L.free()
+    return res
+
+
 def run_copy(args) -> None:
     """Counter calibration: 4 GiB device-to-device copies (HIP's own copy kernel)."""
     n = 4 << 30
@@ -168,9 +361,9 @@ def run_copy(args) -> None:
     b.free()
 
 
-def traffic_from_profile(kernel: str) -> int | None:
-    """HBM bytes per launch of `kernel` from the committed counter summary."""
-    path = os.path.join(ROOT, "profiles", "decode_t1_hbm_traffic.md")
+def traffic_from_profile(kernel: str, summary: str = "decode_t1_hbm_traffic.md") -> int | None:
+    """HBM bytes per launch of `kernel` from a committed counter summary."""
+    path = os.path.join(ROOT, "profiles", summary)
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -182,13 +375,23 @@ def traffic_from_profile(kernel: str) -> int | None:
     return None
 
 
+METRICS = {
+    "decode": METRIC,
+    "batched": "MoE-layer batched-decode tokens/s + HBM GB/s at d=6144, 256e top-8, T=64 Zipf(1.1)",
+    "prefill": "MoE-layer prefill tokens/s + BF16 MFMA TFLOP/s at d=6144, 256e top-8, T=4096",
+    "streamed": "8-layer streamed-expert decode tokens/s + PCIe GB/s at d=6144, 256e top-8",
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="decode", choices=["decode", "copy"])
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=["decode", "batched", "prefill", "streamed", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--distinct-experts", type=int, default=32,
+                    help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -196,16 +399,25 @@ def main() -> int:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
+    defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3), "copy": (5, 0)}
+    d_steps, d_warm = defaults[args.workload]
+    args.steps = d_steps if args.steps is None else args.steps
+    args.warmup = d_warm if args.warmup is None else args.warmup
     capi.call("hfmoe_init", 0)
     if args.workload == "copy":
         run_copy(args)
         capi.load().hfmoe_shutdown()
         return 0
-    res = run_decode(args)
-    line = {"metric": METRIC, "value": round(res.pop("value"), 2), "unit": "tokens/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res.pop("ms_per_step"), 5),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic", **res}
+    if args.workload == "decode":
+        res = run_decode(args)
+    elif args.workload == "streamed":
+        res = run_streamed(args)
+    else:
+        res = run_grouped(args, args.workload)
+    line = {"metric": METRICS[args.workload], "value": round(res.pop("value"), 2), "unit": "tokens/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(res.pop("ms_per_step"), 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic", **res}
     print(json.dumps(line), flush=True)
     capi.load().hfmoe_shutdown()
     return 0

@@ -31,8 +31,8 @@ int fail_hip(hipError_t e, const char* what) {
 
 hipStream_t pick_stream(void* s) { return s ? reinterpret_cast<hipStream_t>(s) : g.stream; }
 
-// ---- profiling: the next launch of a section records its own dispatch
-// timestamps into a pair of pooled events (launch() in hf_kernels.h) ----
+// ---- profiling: the launches of a section record their dispatch timestamps
+// into a pair of pooled events (launch() in hf_kernels.h) ----
 static hipEvent_t pooled_event() {
     hipEvent_t e = nullptr;
     if (!g.event_pool.empty()) {
@@ -65,8 +65,9 @@ void prof_begin(Pending& p, const char* name, hipStream_t s) {
 void prof_end(Pending& p, hipStream_t s) {
     (void)s;
     if (!p.name) return;
-    if (g_timing.start == p.start) {  // nothing was launched in the section
-        g_timing = LaunchTiming{};
+    const bool launched = g_timing.start != p.start;
+    g_timing = LaunchTiming{};
+    if (!launched) {  // nothing was launched in the section
         g.event_pool.push_back(p.start);
         g.event_pool.push_back(p.stop);
         return;
@@ -286,10 +287,17 @@ int hfmoe_register_layer(int layer, const hfmoe_layer_weights* w) {
     st.location = w->experts_location;
     st.host_experts.assign(w->experts, w->experts + 3 * c.E);
     st.norm_w = w->post_attention_norm_dev;
-    hipError_t e = hipMalloc(&st.etab_dev, sizeof(void*) * 3 * (size_t)c.E);
+    // Device table of 3 * (E + 1) pointers: the routed experts' (gate, up,
+    // down), then the shared expert's, which the multi-token path multiplies
+    // as one more group (a single shared expert has a routed expert's shape).
+    hipError_t e = hipMalloc(&st.etab_dev, sizeof(void*) * 3 * (size_t)(c.E + 1));
     if (e != hipSuccess) return fail_hip(e, "hipMalloc(expert table)");
     if (st.location == HFMOE_EXPERTS_DEVICE) {
-        e = hipMemcpy(st.etab_dev, w->experts, sizeof(void*) * 3 * (size_t)c.E, hipMemcpyHostToDevice);
+        std::vector<const void*> tab(w->experts, w->experts + 3 * c.E);
+        tab.push_back(w->shared_gate_dev);
+        tab.push_back(w->shared_up_dev);
+        tab.push_back(w->shared_down_dev);
+        e = hipMemcpy(st.etab_dev, tab.data(), sizeof(void*) * tab.size(), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             hipFree(st.etab_dev);
             return fail_hip(e, "hipMemcpy(expert table)");

@@ -1,28 +1,47 @@
 // dispatch.hip -- token-to-expert dispatch as a stable counting sort (gfx950).
 //
 // The reference has no batched MoE (it loops token by token, glm_forward.cpp:755,
-// and expert by expert, :581); this is the north star's dispatch: pairs
+// and expert by expert, :581); this is the multi-token path's dispatch: pairs
 // p = t*k + r sorted by (expert, p), with per-expert counts and offsets, the
 // same order the CPU oracle's orc_dispatch produces (its stable counting sort).
 //
 // One workgroup of 1024 threads:
 //   1. histogram of experts (LDS atomics: order cannot matter for counts);
-//   2. exclusive scan -> offsets[E+1] and the M-tile list of the grouped GEMM
-//      (ceil(count_e / tile_rows) tiles per expert, in expert order);
+//   2. block-wide exclusive scans of the counts and of the per-expert M-tile
+//      counts ceil(count_e / tile_rows) -> offsets[E+1] and the M-tile list of
+//      the grouped GEMM, in expert order, then the tiles of the shared group;
 //   3. stable scatter, 1024 pairs per pass in pair order: a pair's slot is
 //      cursor[e] + (same-expert pairs in earlier wavefronts of the pass) +
 //      (same-expert pairs in earlier lanes of its wavefront).  The in-wave
 //      match mask comes from one ballot per key bit, so the result is fully
 //      deterministic with no atomics on positions.
 #include "hf_api_internal.h"
+#include "hf_grouped.h"
 
 namespace hf {
 
 constexpr int kDispatchThreads = 1024;
 constexpr int kDispatchWaves = kDispatchThreads / 64;
 
+// Inclusive scan of v over the 1024 threads of the block (wsum: [16] LDS).
+__device__ __forceinline__ int block_scan(int v, int* wsum) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(v, off);
+        if (lane >= off) v += y;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    __syncthreads();
+    return v + before;
+}
+
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
-    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows,
+    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows, int shared_rows,
     int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
     int* __restrict__ row_token, int* __restrict__ tile_expert, int* __restrict__ tile_row0,
     int* __restrict__ ntiles_out) {
@@ -30,6 +49,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     int* cnt = smem;                        // [E]
     int* cursor = cnt + E;                  // [E]
     int* whist = cursor + E;                // [waves][E]
+    __shared__ int wsum[kDispatchWaves];
+    __shared__ int totals[2];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -41,21 +62,48 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (t == 0) {
-        int run = 0, tiles = 0;
-        for (int e = 0; e < E; ++e) {
-            offsets[e] = run;
-            cursor[e] = run;
-            counts[e] = cnt[e];
-            for (int r0 = 0; r0 < cnt[e]; r0 += tile_rows) {
-                tile_expert[tiles] = e;
-                tile_row0[tiles] = run + r0;
-                ++tiles;
+    // Scans over experts in chunks of 1024 (E <= 1024 in practice: one chunk).
+    int run_rows = 0, run_tiles = 0;
+    for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
+        const int e = e0 + t;
+        const int c = e < E ? cnt[e] : 0;
+        const int nt = (c + tile_rows - 1) / tile_rows;
+        const int c_inc = block_scan(c, wsum);
+        const int t_inc = block_scan(nt, wsum);
+        if (e < E) {
+            const int r0 = run_rows + c_inc - c;
+            const int tl0 = run_tiles + t_inc - nt;
+            offsets[e] = r0;
+            cursor[e] = r0;
+            counts[e] = c;
+            for (int j = 0; j < nt; ++j) {
+                tile_expert[tl0 + j] = e;
+                tile_row0[tl0 + j] = r0 + j * tile_rows;
             }
-            run += cnt[e];
         }
-        offsets[E] = run;
-        *ntiles_out = tiles;
+        if (t == kDispatchThreads - 1) {
+            totals[0] = c_inc;
+            totals[1] = t_inc;
+        }
+        __syncthreads();
+        run_rows += totals[0];
+        run_tiles += totals[1];
+        __syncthreads();
+    }
+    // The shared group: rows npairs + i <- token i.
+    const int shared_tiles = (shared_rows + tile_rows - 1) / tile_rows;
+    for (int j = t; j < shared_tiles; j += kDispatchThreads) {
+        tile_expert[run_tiles + j] = E;
+        tile_row0[run_tiles + j] = npairs + j * tile_rows;
+    }
+    for (int i = t; i < shared_rows; i += kDispatchThreads) {
+        perm[npairs + i] = npairs + i;
+        row_token[npairs + i] = i;
+    }
+    if (t == 0) {
+        offsets[E] = run_rows;
+        offsets[E + 1] = run_rows + shared_rows;
+        *ntiles_out = run_tiles + shared_tiles;
     }
     __syncthreads();
 
@@ -92,22 +140,22 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     }
 }
 
-hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int* counts,
-                           int* offsets, int* perm, int* row_token, int* tile_expert,
+hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
+                           int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
                            int* tile_row0, int* ntiles, hipStream_t s) {
     int bits = 1;
     while ((1 << bits) < E) ++bits;
     const size_t lds = sizeof(int) * (size_t)E * (2 + kDispatchWaves);
     static size_t lds_raised = 0;
-    if (lds > 64 * 1024 && lds > lds_raised) {
+    if (lds > 48 * 1024 && lds > lds_raised) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(dispatch_kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         lds_raised = lds;
     }
     return launch(dispatch_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds, s, idx, T * k, k,
-                  E, bits, tile_rows, counts, offsets, perm, row_token, tile_expert, tile_row0,
-                  ntiles);
+                  E, bits, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
+                  tile_row0, ntiles);
 }
 
 }  // namespace hf

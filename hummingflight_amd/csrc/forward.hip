@@ -71,7 +71,7 @@ namespace hf {
 
 // Multi-token forward, token by token over the decode kernels (every token
 // re-streams its experts' weights): used for shapes the grouped GEMM does not
-// tile (hidden or intermediate not a multiple of 32).
+// tile (hidden or intermediate not a multiple of 64).
 int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                       const hfmoe_route_debug* dbg) {
     const Cfg& c = g.cfg;

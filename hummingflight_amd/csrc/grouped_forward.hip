@@ -7,10 +7,10 @@
 //      then score pairs (sigmoid, sigmoid + bias)
 //   3. per-token selection (hf_select.h), one block per token
 //   4. dispatch: stable counting sort of (token, rank) pairs by expert
-//   5. routed gate/up grouped GEMM -> h (BF16 hi/lo, sorted rows)
-//   6. shared-expert gate/up GEMM over all tokens -> shared h
-//   7. routed down grouped GEMM -> y at each pair's slot [T*k, d]
-//   8. shared down GEMM fused with the combine: out[t] = sum_r w*y + shared
+//   5. gate/up grouped GEMM over the routed groups plus the shared expert as
+//      one more group -> h (BF16 hi/lo, sorted rows)
+//   6. down grouped GEMM -> y at each pair's slot [T*k, d], shared rows after
+//   7. combine: out[t] = (sum_r w[t,r] * y[t*k + r]) + y[T*k + t]
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 
@@ -18,27 +18,39 @@ namespace hf {
 
 static bool grouped_supported() {
     const Cfg& c = g.cfg;
-    return c.d % 32 == 0 && c.I % 32 == 0;
+    return c.d % kGemmTileK == 0 && c.I % kGemmTileK == 0 && c.n_shared <= 1;
 }
 
-// Split-K factor of the router GEMM: enough (tile, split) items for every CU.
+// Split-K factor of the router GEMM: enough (tile, split) items for every CU,
+// each split at least 4 K stages long.
 static int router_ksplit(int T) {
     const Cfg& c = g.cfg;
     const int tiles = ((T + kGemmTileRows - 1) / kGemmTileRows) * ((c.E + 127) / 128);
-    const int kmax = c.d / 32;
+    const int kmax = c.d / kGemmTileK;
     const int want = (2 * g.num_cus + tiles - 1) / tiles;
     int best = 1;
-    for (int ks = 1; ks <= kmax && ks <= want; ++ks)
+    for (int ks = 1; ks <= kmax / 4 && ks <= want; ++ks)
         if (kmax % ks == 0) best = ks;
     return best;
 }
 
-static int gemm_blocks() { return env_int("HFMOE_GEMM_BLOCKS", g.num_cus * 2); }
+// Persistent grid: two 4-wave workgroups per CU (128-row tiles) or one 8-wave
+// workgroup per CU (256-row tiles).
+static int gemm_blocks(int tile_rows) {
+    return env_int("HFMOE_GEMM_BLOCKS", tile_rows == 256 ? g.num_cus : g.num_cus * 2);
+}
+
+// 256-row tiles once experts average 96+ rows (prefill): an expert's rows then
+// fit one tile and its weights stream through the memory system once.
+static int expert_tile_rows(int T) {
+    const Cfg& c = g.cfg;
+    return (size_t)T * c.k >= (size_t)96 * c.E ? 256 : kGemmTileRows;
+}
 
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.shh, w.shl, w.part};
+                    w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -50,9 +62,10 @@ int grouped_workspace_alloc() {
     const int T = g.max_tokens;
     if (T <= 1 || !grouped_supported()) return HFMOE_OK;
     GroupedWorkspace& w = g.gws;
-    const size_t P = (size_t)T * c.k;
-    const size_t Is = (size_t)c.n_shared * c.I;
-    w.max_tiles = c.E + (int)((P + kGemmTileRows - 1) / kGemmTileRows);
+    // Sorted rows: T*k routed (token, rank) pairs, then T shared-expert rows.
+    const size_t R = (size_t)T * c.k + (size_t)T * c.n_shared;
+    w.max_tiles = c.E + 1 + (int)(((size_t)T * c.k + kGemmTileRows - 1) / kGemmTileRows) +
+                  (T + kGemmTileRows - 1) / kGemmTileRows;
     size_t tks = 0;
     for (int t = 2; t <= T; ++t) tks = std::max(tks, (size_t)t * router_ksplit(t));
     struct A {
@@ -60,20 +73,18 @@ int grouped_workspace_alloc() {
         size_t bytes;
     } list[] = {
         {(void**)&w.counts, sizeof(int) * c.E},
-        {(void**)&w.offsets, sizeof(int) * (c.E + 1)},
-        {(void**)&w.perm, sizeof(int) * P},
-        {(void**)&w.row_token, sizeof(int) * P},
+        {(void**)&w.offsets, sizeof(int) * (c.E + 2)},
+        {(void**)&w.perm, sizeof(int) * R},
+        {(void**)&w.row_token, sizeof(int) * R},
         {(void**)&w.tile_expert, sizeof(int) * w.max_tiles},
         {(void**)&w.tile_row0, sizeof(int) * w.max_tiles},
         {(void**)&w.ntiles, 256},
         {(void**)&w.lo_flag, 256},
         {(void**)&w.xh, 2 * (size_t)T * c.d},
         {(void**)&w.xl, 2 * (size_t)T * c.d},
-        {(void**)&w.hh, 2 * P * c.I},
-        {(void**)&w.hl, 2 * P * c.I},
-        {(void**)&w.y, 4 * P * c.d},
-        {(void**)&w.shh, 2 * (size_t)T * (Is ? Is : 1)},
-        {(void**)&w.shl, 2 * (size_t)T * (Is ? Is : 1)},
+        {(void**)&w.hh, 2 * R * c.I},
+        {(void**)&w.hl, 2 * R * c.I},
+        {(void**)&w.y, 4 * R * c.d},
         {(void**)&w.part, 4 * tks * c.E},
     };
     for (auto& a : list) {
@@ -87,21 +98,10 @@ int grouped_workspace_alloc() {
     return HFMOE_OK;
 }
 
-// out[t] = sum_r w[t, r] * y[t*k + r] when there is no shared expert to fuse with.
-__global__ void combine_kernel(const float* __restrict__ wts, const float* __restrict__ y, int T,
-                               int k, int d, float* __restrict__ out) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)T * d) return;
-    const size_t t = i / d, n = i % d;
-    float moe = 0.0f;
-    for (int r = 0; r < k; ++r) moe += wts[t * k + r] * y[(t * k + r) * d + n];
-    out[i] = moe;
-}
-
-#define HF_CHECK_LAUNCH(expr, what)                  \
-    do {                                             \
-        hipError_t e_ = (expr);                      \
-        prof_end(p, s);                              \
+#define HF_CHECK_LAUNCH(expr, what)                      \
+    do {                                                 \
+        hipError_t e_ = (expr);                          \
+        prof_end(p, s);                                  \
         if (e_ != hipSuccess) return fail_hip(e_, what); \
     } while (0)
 
@@ -110,8 +110,9 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     if (!g.gws.xh) return forward_tokenwise(L, x, T, out, s, dbg);
     const Cfg& c = g.cfg;
     GroupedWorkspace& w = g.gws;
-    const int Is = c.n_shared * c.I;
-    const int blocks = gemm_blocks();
+    const int P = T * c.k;
+    const int shared_rows = c.n_shared > 0 ? T : 0;
+    const int TR = expert_tile_rows(T);
     Pending p;
 
     prof_begin(p, "split_x", s);
@@ -121,6 +122,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     GemmArgs r{};
     r.K = c.d;
     r.N = c.E;
+    r.tile_rows = kGemmTileRows;
     r.n_tiles = (c.E + 127) / 128;
     r.m_tiles = (T + kGemmTileRows - 1) / kGemmTileRows;
     r.rows_total = T;
@@ -132,26 +134,30 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     r.out_f32 = w.part;
     r.ksplit = ks;
     prof_begin(p, "router_gemm", s);
-    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, r, blocks, s), "router gemm");
+    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, r, gemm_blocks(kGemmTileRows), s), "router gemm");
     prof_begin(p, "router_reduce", s);
     HF_CHECK_LAUNCH(launch_router_reduce(w.part, ks, T, c.E, L.dev.bias, g.ws.logits, g.ws.scores, s),
                     "router reduce");
     prof_begin(p, "select", s);
     HF_CHECK_LAUNCH(launch_select(g.ws.scores, T, c, g.ws.idx, g.ws.wts, s), "select");
     prof_begin(p, "dispatch", s);
-    HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, kGemmTileRows, w.counts, w.offsets, w.perm,
-                                    w.row_token, w.tile_expert, w.tile_row0, w.ntiles, s),
+    HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, TR, shared_rows, w.counts,
+                                    w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0,
+                                    w.ntiles, s),
                     "dispatch");
 
+    // Gate/up of every group: the routed experts' (token, rank) rows and the
+    // shared expert's token rows (group E), one launch.
     GemmArgs gu{};
     gu.K = c.d;
     gu.N = c.I;
+    gu.tile_rows = TR;
     gu.n_tiles = (c.I + 63) / 64;
     gu.tile_group = w.tile_expert;
     gu.tile_row0 = w.tile_row0;
     gu.ntiles_dev = w.ntiles;
     gu.group_end = w.offsets + 1;
-    gu.rows_total = T * c.k;
+    gu.rows_total = P + shared_rows;
     gu.a_hi = w.xh;
     gu.a_lo = w.xl;
     gu.a_lo_flag = w.lo_flag;
@@ -163,37 +169,20 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     prof_begin(p, "expert_gateup_gemm", s);
-    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, blocks, s), "routed gate/up gemm");
+    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
 
-    if (c.n_shared > 0) {
-        GemmArgs sg{};
-        sg.K = c.d;
-        sg.N = Is;
-        sg.n_tiles = (Is + 63) / 64;
-        sg.m_tiles = (T + kGemmTileRows - 1) / kGemmTileRows;
-        sg.rows_total = T;
-        sg.a_hi = w.xh;
-        sg.a_lo = w.xl;
-        sg.a_lo_flag = w.lo_flag;
-        sg.b_fixed0 = L.dev.sg;
-        sg.b_fixed1 = L.dev.su;
-        sg.b_ld = c.d;
-        sg.h_hi = w.shh;
-        sg.h_lo = w.shl;
-        sg.ksplit = 1;
-        prof_begin(p, "shared_gateup_gemm", s);
-        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, sg, blocks, s), "shared gate/up gemm");
-    }
-
+    // Down projections of every group; row r's output lands at row perm[r] of
+    // y: pair slot t*k + r for routed rows, T*k + t for the shared expert.
     GemmArgs dn{};
     dn.K = c.I;
     dn.N = c.d;
+    dn.tile_rows = TR;
     dn.n_tiles = (c.d + 127) / 128;
     dn.tile_group = w.tile_expert;
     dn.tile_row0 = w.tile_row0;
     dn.ntiles_dev = w.ntiles;
     dn.group_end = w.offsets + 1;
-    dn.rows_total = T * c.k;
+    dn.rows_total = P + shared_rows;
     dn.a_hi = w.hh;
     dn.a_lo = w.hl;
     dn.b_tab = L.dev.etab;
@@ -203,33 +192,10 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     prof_begin(p, "expert_down_gemm", s);
-    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, blocks, s), "routed down gemm");
+    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
 
-    if (c.n_shared > 0) {
-        GemmArgs sd{};
-        sd.K = Is;
-        sd.N = c.d;
-        sd.n_tiles = (c.d + 127) / 128;
-        sd.m_tiles = (T + kGemmTileRows - 1) / kGemmTileRows;
-        sd.rows_total = T;
-        sd.a_hi = w.shh;
-        sd.a_lo = w.shl;
-        sd.b_fixed0 = L.dev.sd;
-        sd.b_ld = Is;
-        sd.out_f32 = out;
-        sd.comb_w = g.ws.wts;
-        sd.comb_y = w.y;
-        sd.comb_k = c.k;
-        sd.ksplit = 1;
-        prof_begin(p, "shared_down_combine_gemm", s);
-        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_COMBINE, sd, blocks, s), "shared down + combine gemm");
-    } else {
-        const size_t n = (size_t)T * c.d;
-        prof_begin(p, "combine", s);
-        HF_CHECK_LAUNCH(launch(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                               g.ws.wts, w.y, T, c.k, c.d, out),
-                        "combine");
-    }
+    prof_begin(p, "combine", s);
+    HF_CHECK_LAUNCH(launch_combine(g.ws.wts, w.y, T, c.k, c.d, shared_rows ? P : -1, out, s), "combine");
     return copy_debug(dbg, T, s);
 }
 

@@ -12,50 +12,302 @@
 // SwiGLU intermediate h always uses both halves (BF16 h alone misses the
 // 1e-2/2e-3 tolerance at d = 6144).
 //
-// Tile 128 x 128 x 32, 256 threads as 2 x 2 wavefronts of 64 x 64 (4 x 4
-// MFMA tiles of 16 x 16), LDS double-buffered, persistent workgroups walking a
-// contiguous range of (m-tile, n-tile) items per XCD so that neighbouring
-// tiles of one expert share that XCD's L2.
+// The MoE GEMMs stream expert weights (B) far more than they compute: at
+// T = 4096 each expert sees ~128 rows, 128 FLOP per weight byte, below the
+// MI355X ridge (~312), and at T = 64 a few rows.  So the kernel is built to
+// keep B streaming and to spend MFMA cycles only on rows that exist:
+//   * tile 128 or 256 (M) x 128 (N) x 64 (K), 4 or 8 wavefronts; wavefront w
+//     owns tile rows [32w, 32w + 32) across all 128 columns and skips the
+//     MFMAs of 16-row blocks past the group's last row, so a 3-row expert
+//     costs one 16-row block of work, not 128;
+//   * B goes straight from global memory into an LDS ring by DMA
+//     (global_load_lds_dwordx4) with no register staging, and A fragments
+//     straight into registers (L2-resident activations, row-gathered through
+//     a_rowmap); both are fetched 2-4 K stages ahead of the one multiplied;
+//   * persistent workgroups walk a contiguous range of (m-tile, n-tile) items
+//     per XCD, n fastest, so an M tile's activations and the B slices shared
+//     by an expert's M tiles are reused within that XCD's L2.
 //
 // Epilogues:
 //   PARTIAL  split-K partial sums (router logits; reduced in fixed order later)
 //   SWIGLU   B rows = 64 gate rows then the 64 matching up rows; writes
 //            h = silu(g) * u as BF16 hi/lo (glm_forward.cpp:444-446)
-//   SCATTER  y for one (token, rank) pair per row, stored at its pair slot
-//   COMBINE  shared-expert down projection + the weighted merge: out[t] =
-//            (sum_r w[t,r] * y[t,r]) + shared[t] in rank order
-//            (glm_forward.cpp:639-640,658-660)
+//   SCATTER  y for one (token, rank) pair per row, stored at row scatter_rows[r]
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 #include "hf_select.h"
+
+#include <type_traits>
 
 namespace hf {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int GBM = kGemmTileRows, GBN = 128, GBK = 32, GLD = GBK + 8;
-
-struct GemmSmem {
-    uint16_t a_hi[2][GBM][GLD];
-    uint16_t a_lo[2][GBM][GLD];
-    uint16_t b[2][GBN][GLD];
-};
+constexpr int GBN = 128, GBK = kGemmTileK;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-__device__ __forceinline__ u32x4 lds_frag(const uint16_t* p) {
-    return *reinterpret_cast<const u32x4*>(p);
+// 16-byte load through a global-address-space pointer.  Pointers read from
+// memory (the expert table) are generic; a generic load is a FLAT instruction,
+// which also counts against the LDS counter and is not ordered with other
+// vector loads, so every LDS wait would drain the weight prefetch.
+__device__ __forceinline__ u32x4 ld_global(const uint16_t* p) {
+    return *(const __attribute__((address_space(1))) u32x4*)(p);
 }
 
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GemmArgs a) {
-    __shared__ GemmSmem sm;
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+// B stages in LDS: 128 rows x 64 k of BF16, 128-byte rows whose 16-byte
+// chunks are XOR-swizzled by (row & 7), which keeps both the DMA writes
+// (lane-contiguous) and the fragment reads (16 rows x 16 bytes per quarter
+// wave) free of bank conflicts.
+constexpr int kDmaPolicy = 2;  // cache-policy bits of the weight DMA: non-temporal
+typedef uint16_t BStage[GBN * GBK];
+// Prefetch distance (K stages) of A and B: deeper when only the hi half of A
+// is multiplied (half the MFMA work per stage, same bytes); the ring holds
+// distance + 1 stages.
+constexpr int kDepthHi = 4, kDepthLo = 2;
+constexpr size_t kRingBytes = sizeof(BStage) * (kDepthHi + 1);
+
+// Weight DMA with the non-temporal hint: each weight tile is read by at most
+// the few M tiles of one expert, close together in time, while the activation
+// rows are re-read by every N tile of their M tile and must stay in L2.
+__device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* l) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)l, 16, 0, kDmaPolicy);
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without the release fence of __syncthreads(), which would
+// drain every outstanding load (the weight DMA of later stages included);
+// the asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// One (m-tile, n-tile, k-split) item.  USE_LO: multiply the A lo half too.
+//
+// Pipeline per K stage s (64 k), prefetch distance D: every wave waits until
+// its A registers and its DMA of B for stage s have landed, the workgroup
+// meets at a barrier, then each wave issues A of stage s+D (registers) and
+// its quarter of B stage s+D (DMA into the ring slot stage s-1 used), and
+// multiplies stage s.  A and B of one stage are issued together, so waiting
+// for stage s (in-order load counter) never waits for a later stage.
+template <int EPI, bool USE_LO, int WAVES>
+__device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* ring, int t, int wave) {
+    constexpr int GBM = 32 * WAVES;     // tile rows: 32 per wavefront
+    constexpr int BJ = 16 / WAVES;      // 1 KB weight DMAs per wave per stage
     constexpr int cols_per_tile = EPI == EPI_SWIGLU ? GBN / 2 : GBN;
+    constexpr int NA = USE_LO ? 8 : 4;  // A loads per wave per stage
+    constexpr int D = USE_LO ? kDepthLo : kDepthHi;
+    constexpr int RING = D + 1;
+    const int lane = t & 63;
+    const int fr = lane & 15;  // fragment row (A) / column (B, D)
+    const int fq = lane >> 4;  // fragment k quarter
+    const int Kc = a.K / a.ksplit;
+    const int nk = Kc / GBK;
+
+    const int ks = item % a.ksplit;
+    const int rest = item / a.ksplit;
+    const int nt = rest % a.n_tiles;
+    const int mt = rest / a.n_tiles;
+    const int g = a.tile_group ? a.tile_group[mt] : 0;
+    const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * GBM;
+    const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
+    const int rows = min(GBM, row_end - row0);
+    const int n0 = nt * cols_per_tile;
+    const uint16_t* b0;
+    const uint16_t* b1 = nullptr;
+    if (a.b_tab) {
+        b0 = a.b_tab[3 * g + a.b_which];
+        if (EPI == EPI_SWIGLU) b1 = a.b_tab[3 * g + a.b_which + 1];
+    } else {
+        b0 = a.b_fixed0;
+        b1 = a.b_fixed1;
+    }
+    const int kbase = ks * Kc;
+    // 16-row blocks of this wavefront that hold rows (0, 1 or 2; wave-uniform).
+    const int wrows = min(max(rows - 32 * wave, 0), 32);
+    const int nrb = (wrows + 15) >> 4;
+
+    // A fragment sources: lane row fr of row blocks 0 and 1, clamped to the
+    // tile's last row (rows past it are loaded but never multiplied or stored).
+    const uint16_t* ap[2];
+    const uint16_t* alp[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int lr = min(32 * wave + 16 * rb + fr, rows - 1);
+        const int gr = row0 + lr;
+        const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
+        ap[rb] = a.a_hi + src * a.K + kbase + fq * 8;
+        alp[rb] = USE_LO ? a.a_lo + src * a.K + kbase + fq * 8 : nullptr;
+    }
+    // B DMA sources: wave w fills ring slots (BJ*w + j) * 64 + lane, j < BJ,
+    // each 16 bytes: slot i holds chunk (i & 7) ^ (row & 7) of tile row i >> 3.
+    // Rows past N are clamped to row N-1 (their columns are never stored).
+    const uint16_t* bsrc[BJ];
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+        const int i = (wave * BJ + j) * 64 + lane;
+        const int r = i >> 3;
+        const int c = (i & 7) ^ (r & 7);
+        const uint16_t* base = b0;
+        int n;
+        if (EPI == EPI_SWIGLU) {
+            n = n0 + (r & 63);
+            if (r >= 64) base = b1;
+        } else {
+            n = n0 + r;
+        }
+        n = min(n, a.N - 1);
+        bsrc[j] = base + (size_t)n * a.b_ld + kbase + c * 8;
+    }
+
+    f32x4_t acc[2][8];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) acc[rb][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Loads are unconditional (stage indices clamped to the last stage) so the
+    // number of loads in flight, which the counter waits rely on, is fixed.
+    auto issue_b = [&](int s) {
+        uint16_t* dst = ring[s % RING] + wave * BJ * 512;
+        s = min(s, nk - 1);
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) dma16(bsrc[j] + s * GBK, dst + j * 512);
+    };
+    typedef u32x4 AFrag[2][2][2];  // [hi/lo][row block][k half]
+    auto load_a = [&](AFrag& f, int s) {
+        s = min(s, nk - 1);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                f[0][rb][kh] = ld_global(ap[rb] + s * GBK + kh * 32);
+                if (USE_LO) f[1][rb][kh] = ld_global(alp[rb] + s * GBK + kh * 32);
+            }
+    };
+    // Four groups of four column blocks (k half kh = g >> 1, column half
+    // ch = g & 1); the B fragments of group g+1 are read from LDS while the
+    // MFMAs of group g run.
+    auto compute = [&](const uint16_t* bt, const AFrag& f) {
+        if (nrb == 0) return;
+        bf16x8_t bf[2][4];
+        auto read_group = [&](int g, bf16x8_t(&dst)[4]) {
+            const int kh = g >> 1, ch = g & 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 16 * (4 * ch + j) + fr;
+                const int c = (kh * 4 + fq) ^ (r & 7);
+                dst[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
+            }
+        };
+        read_group(0, bf[0]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if (g + 1 < 4) read_group(g + 1, bf[(g + 1) & 1]);
+            const int kh = g >> 1, ch = g & 1;
+            const bf16x8_t(&b)[4] = bf[g & 1];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                if (rb == 1 && nrb < 2) break;
+                const bf16x8_t af = as_bf16x8(f[0][rb][kh]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[rb][4 * ch + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[j], acc[rb][4 * ch + j], 0, 0, 0);
+                if (USE_LO) {
+                    const bf16x8_t alf = as_bf16x8(f[1][rb][kh]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[rb][4 * ch + j] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(alf, b[j], acc[rb][4 * ch + j], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // Steady-state steps wait for stage s with stages s+1 .. s+D-1 still in
+    // flight.  Tail steps (after the loop) drain instead: the compiler drops
+    // the A loads whose registers are never read again, so the count of
+    // loads issued after stage s is no longer fixed there.
+    auto step = [&](int s, const AFrag& cur, AFrag& ahead, auto tail) {
+        if constexpr (decltype(tail)::value)
+            wait_vmcnt<0>();
+        else
+            wait_vmcnt<(D - 1) * (NA + BJ)>();
+        lds_barrier();
+        load_a(ahead, s + D);
+        issue_b(s + D);
+        compute(ring[s % RING], cur);
+    };
+
+    AFrag A[RING];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load_a(A[j], j);
+        issue_b(j);
+    }
+    // Whole rotations only inside the loop: a back edge that always follows
+    // the same steps lets the compiler's own counter waits stay exact.
+    int s = 0;
+    for (; s + RING <= nk; s += RING) {
+#pragma unroll
+        for (int u = 0; u < RING; ++u) step(s + u, A[u], A[(u + D) % RING], std::false_type{});
+    }
+#pragma unroll
+    for (int u = 0; u < RING - 1; ++u)
+        if (s + u < nk) step(s + u, A[u], A[(u + D) % RING], std::true_type{});
+
+    // Epilogue: lane holds D[4*fq + q][fr] of each 16 x 16 block.
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        if (rb >= nrb) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rl_ = 32 * wave + 16 * rb + 4 * fq + q;
+            if (rl_ >= rows) continue;
+            const int gr = row0 + rl_;
+            if (EPI == EPI_SWIGLU) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const int col = n0 + 16 * cb + fr;
+                    if (col >= a.N) continue;
+                    const float gv = acc[rb][cb][q];
+                    const float uv = acc[rb][cb + 4][q];
+                    const float hv = gv / (1.0f + expf(-gv)) * uv;
+                    const uint16_t hb = f32_to_bf16(hv);
+                    const float hr = hv - __uint_as_float((uint32_t)hb << 16);
+                    a.h_hi[(size_t)gr * a.N + col] = hb;
+                    a.h_lo[(size_t)gr * a.N + col] = f32_to_bf16(hr);
+                }
+            } else {
+                float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
+                                                 : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) {
+                    const int col = n0 + 16 * cb + fr;
+                    if (col < a.N) orow[col] = acc[rb][cb][q];
+                }
+            }
+        }
+    }
+}
+
+// WAVES = 4: 128-row tiles, two workgroups per CU; WAVES = 8: 256-row tiles
+// (one expert's rows in one tile at prefill sizes, so each weight tile
+// crosses the memory system once), one workgroup per CU.
+template <int EPI, bool LO, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) BStage ring[];  // kRingBytes
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar branches
 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const int total = m_tiles * a.n_tiles * a.ksplit;
@@ -67,169 +319,44 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GemmArgs a) {
     const int chunk = (total + nxcd - 1) / nxcd;
     const int item_begin = xcd * chunk;
     const int item_end = min(total, item_begin + chunk);
-    const bool use_lo = a.a_lo && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
-    const int Kc = a.K / a.ksplit;
-    const int nk = Kc / GBK;
-
-    // Loader mapping: thread t fills 16 bytes of rows (t >> 2) and (t >> 2) + 64.
-    const int lrow = t >> 2;
-    const int lc = (t & 3) * 8;
+    // The lo half is multiplied only when present (x that is BF16-valued has none).
+    const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
 
     for (int item = item_begin + local; item < item_end; item += per_xcd_blocks) {
-        const int ks = item % a.ksplit;
-        const int rest = item / a.ksplit;
-        const int nt = rest % a.n_tiles;
-        const int mt = rest / a.n_tiles;
-        const int g = a.tile_group ? a.tile_group[mt] : 0;
-        const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * GBM;
-        const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
-        const int rows = min(GBM, row_end - row0);
-        const int n0 = nt * cols_per_tile;
-        const uint16_t* b0;
-        const uint16_t* b1 = nullptr;
-        if (a.b_tab) {
-            b0 = a.b_tab[3 * g + a.b_which];
-            if (EPI == EPI_SWIGLU) b1 = a.b_tab[3 * g + a.b_which + 1];
-        } else {
-            b0 = a.b_fixed0;
-            b1 = a.b_fixed1;
-        }
-        const int kbase = ks * Kc;
-
-        // Global source rows of this thread's two A rows and two B rows.
-        const uint16_t* ah[2];
-        const uint16_t* al[2];
-        const uint16_t* bp[2];
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-            const int r = lrow + 64 * h2;
-            ah[h2] = nullptr;
-            al[h2] = nullptr;
-            if (r < rows) {
-                const int gr = row0 + r;
-                const int src = a.a_rowmap ? a.a_rowmap[gr] : gr;
-                ah[h2] = a.a_hi + (size_t)src * a.K + kbase + lc;
-                if (use_lo) al[h2] = a.a_lo + (size_t)src * a.K + kbase + lc;
-            }
-            bp[h2] = nullptr;
-            if (EPI == EPI_SWIGLU) {
-                const int n = n0 + (r & 63);
-                if (n < a.N) bp[h2] = (r < 64 ? b0 : b1) + (size_t)n * a.b_ld + kbase + lc;
-            } else {
-                const int n = n0 + r;
-                if (n < a.N) bp[h2] = b0 + (size_t)n * a.b_ld + kbase + lc;
-            }
-        }
-
-        u32x4 ra[2], rl[2], rb[2];
-        auto gload = [&](int kt) {
-            const int ko = kt * GBK;
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const u32x4 zero = {0u, 0u, 0u, 0u};
-                ra[h2] = ah[h2] ? *reinterpret_cast<const u32x4*>(ah[h2] + ko) : zero;
-                rl[h2] = al[h2] ? *reinterpret_cast<const u32x4*>(al[h2] + ko) : zero;
-                rb[h2] = bp[h2] ? ld_stream(reinterpret_cast<const u32x4*>(bp[h2] + ko)) : zero;
-            }
-        };
-        auto lstore = [&](int buf) {
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const int r = lrow + 64 * h2;
-                *reinterpret_cast<u32x4*>(&sm.a_hi[buf][r][lc]) = ra[h2];
-                if (use_lo) *reinterpret_cast<u32x4*>(&sm.a_lo[buf][r][lc]) = rl[h2];
-                *reinterpret_cast<u32x4*>(&sm.b[buf][r][lc]) = rb[h2];
-            }
-        };
-
-        f32x4_t acc[4][4];
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-
-        // B-tile row bases of this wavefront's four 16-column subtiles.
-        int nb[4];
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-            nb[ni] = EPI == EPI_SWIGLU ? (ni < 2 ? wn * 32 + 16 * ni : 64 + wn * 32 + 16 * (ni - 2))
-                                       : wn * 64 + 16 * ni;
-        const int fr = lane & 15;
-        const int fk = (lane >> 4) * 8;
-
-        gload(0);
-        lstore(0);
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < nk) gload(kt + 1);
-            bf16x8_t af[4], bfr[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) af[mi] = as_bf16x8(lds_frag(&sm.a_hi[buf][wm * 64 + 16 * mi + fr][fk]));
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) bfr[ni] = as_bf16x8(lds_frag(&sm.b[buf][nb[ni] + fr][fk]));
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
-            if (use_lo) {
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi) af[mi] = as_bf16x8(lds_frag(&sm.a_lo[buf][wm * 64 + 16 * mi + fr][fk]));
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                    for (int ni = 0; ni < 4; ++ni)
-                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
-            }
-            if (kt + 1 < nk) lstore(buf ^ 1);
-            __syncthreads();
-        }
-
-        // Epilogue: lane holds D[4*(lane>>4) + q][lane & 15] of each 16 x 16 tile.
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int rl_ = wm * 64 + 16 * mi + 4 * (lane >> 4) + q;
-                if (rl_ >= rows) continue;
-                const int gr = row0 + rl_;
-                if (EPI == EPI_SWIGLU) {
-#pragma unroll
-                    for (int ni = 0; ni < 2; ++ni) {
-                        const int col = n0 + wn * 32 + 16 * ni + fr;
-                        if (col >= a.N) continue;
-                        const float gv = acc[mi][ni][q];
-                        const float uv = acc[mi][ni + 2][q];
-                        const float hv = gv / (1.0f + expf(-gv)) * uv;
-                        const uint16_t hb = f32_to_bf16(hv);
-                        const float hr = hv - __uint_as_float((uint32_t)hb << 16);
-                        a.h_hi[(size_t)gr * a.N + col] = hb;
-                        a.h_lo[(size_t)gr * a.N + col] = f32_to_bf16(hr);
-                    }
-                } else {
-#pragma unroll
-                    for (int ni = 0; ni < 4; ++ni) {
-                        const int col = n0 + wn * 64 + 16 * ni + fr;
-                        if (col >= a.N) continue;
-                        const float v = acc[mi][ni][q];
-                        if (EPI == EPI_PARTIAL) {
-                            a.out_f32[((size_t)ks * a.rows_total + gr) * a.N + col] = v;
-                        } else if (EPI == EPI_SCATTER) {
-                            a.out_f32[(size_t)a.scatter_rows[gr] * a.N + col] = v;
-                        } else {
-                            float moe = 0.0f;
-                            for (int r = 0; r < a.comb_k; ++r)
-                                moe += a.comb_w[(size_t)gr * a.comb_k + r] *
-                                       a.comb_y[((size_t)gr * a.comb_k + r) * a.N + col];
-                            a.out_f32[(size_t)gr * a.N + col] = moe + v;
-                        }
-                    }
-                }
-            }
-        }
-        __syncthreads();
+        if (use_lo)
+            gemm_item<EPI, LO, WAVES>(a, item, ring, t, wave);
+        else
+            gemm_item<EPI, false, WAVES>(a, item, ring, t, wave);
+        __syncthreads();  // all DMA landed and all ring reads done before the next item
     }
+}
+
+// out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):
+// the weighted merge in rank order, then the shared expert (glm_forward.cpp:639-640, 658-660).
+__global__ void combine_kernel(const float* __restrict__ wts, const float* __restrict__ y, int T, int k,
+                               int d, int shared_row0, float* __restrict__ out) {
+    const size_t i4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int d4 = d >> 2;
+    if (i4 >= (size_t)T * d4) return;
+    const int t = (int)(i4 / d4), n4 = (int)(i4 % d4);
+    const float4* y4 = reinterpret_cast<const float4*>(y);
+    float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int r = 0; r < k; ++r) {
+        const float w = wts[(size_t)t * k + r];
+        const float4 v = y4[((size_t)t * k + r) * d4 + n4];
+        m.x += w * v.x;
+        m.y += w * v.y;
+        m.z += w * v.z;
+        m.w += w * v.w;
+    }
+    if (shared_row0 >= 0) {
+        const float4 v = y4[((size_t)shared_row0 + t) * d4 + n4];
+        m.x += v.x;
+        m.y += v.y;
+        m.z += v.z;
+        m.w += v.w;
+    }
+    reinterpret_cast<float4*>(out)[i4] = m;
 }
 
 // x FP32 [n] -> BF16 hi/lo; *flag |= 1 when any lo is nonzero.
@@ -264,14 +391,42 @@ __global__ void router_reduce_kernel(const float* __restrict__ part, int ksplit,
     scores[i] = score_pair(s, bias, i % E);
 }
 
+template <int EPI, bool LO, int WAVES>
+static hipError_t launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
+    static bool raised = false;  // the ring exceeds the default 64 KB of dynamic LDS
+    if (!raised) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<EPI, LO, WAVES>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRingBytes);
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    return launch(grouped_gemm_kernel<EPI, LO, WAVES>, dim3(blocks), dim3(64 * WAVES), (uint32_t)kRingBytes, s, a);
+}
+
+template <int EPI>
+static hipError_t launch_epi(const GemmArgs& a, int blocks, hipStream_t s) {
+    const bool lo = a.a_lo != nullptr;
+    if (a.tile_rows == 256)
+        return lo ? launch_gemm<EPI, true, 8>(a, blocks, s) : launch_gemm<EPI, false, 8>(a, blocks, s);
+    if (a.tile_rows == 128)
+        return lo ? launch_gemm<EPI, true, 4>(a, blocks, s) : launch_gemm<EPI, false, 4>(a, blocks, s);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s) {
     switch (epi) {
-        case EPI_PARTIAL: return launch(grouped_gemm_kernel<EPI_PARTIAL>, dim3(blocks), dim3(256), 0, s, a);
-        case EPI_SWIGLU: return launch(grouped_gemm_kernel<EPI_SWIGLU>, dim3(blocks), dim3(256), 0, s, a);
-        case EPI_SCATTER: return launch(grouped_gemm_kernel<EPI_SCATTER>, dim3(blocks), dim3(256), 0, s, a);
-        case EPI_COMBINE: return launch(grouped_gemm_kernel<EPI_COMBINE>, dim3(blocks), dim3(256), 0, s, a);
+        case EPI_PARTIAL: return launch_epi<EPI_PARTIAL>(a, blocks, s);
+        case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, blocks, s);
+        case EPI_SCATTER: return launch_epi<EPI_SCATTER>(a, blocks, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d, int shared_row0,
+                          float* out, hipStream_t s) {
+    const size_t n4 = (size_t)T * (d / 4);
+    return launch(combine_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, wts, y, T, k, d,
+                  shared_row0, out);
 }
 
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,

@@ -26,26 +26,24 @@ struct Workspace {
     float* tmp = nullptr;        // [2, maxT, d] (mlp block: normed x, MoE out)
 };
 
-// Buffers of the multi-token (dispatch + grouped) path.
+// Buffers of the multi-token (dispatch + grouped) path.  Sorted rows: the
+// maxT*k routed (token, rank) pairs by expert, then maxT shared-expert rows.
 struct GroupedWorkspace {
     int* counts = nullptr;       // [E]
-    int* offsets = nullptr;      // [E + 1]
-    int* perm = nullptr;         // [maxT*k] pair ids in (expert, pair) order
-    int* row_token = nullptr;    // [maxT*k] token of each sorted row
-    int* tile_expert = nullptr;  // [max_tiles] expert of each 128-row M tile
+    int* offsets = nullptr;      // [E + 2] group row offsets (group E = shared expert)
+    int* perm = nullptr;         // [rows] pair id (y row) of each sorted row
+    int* row_token = nullptr;    // [rows] token of each sorted row
+    int* tile_expert = nullptr;  // [max_tiles] group of each 128-row M tile
     int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
     int* ntiles = nullptr;       // [1] M tiles in use
     unsigned int* lo_flag = nullptr;  // [1] x has a nonzero BF16 lo half
     uint16_t* xh = nullptr;      // [maxT, d] x BF16 hi (token order)
     uint16_t* xl = nullptr;      // [maxT, d] x BF16 lo
-    uint16_t* hh = nullptr;      // [maxT*k, I] h hi (sorted rows)
-    uint16_t* hl = nullptr;      // [maxT*k, I] h lo
-    float* y = nullptr;          // [maxT*k, d] per-pair expert outputs at pair slots
-    uint16_t* shh = nullptr;     // [maxT, S*I] shared-expert h hi / lo
-    uint16_t* shl = nullptr;
+    uint16_t* hh = nullptr;      // [rows, I] h hi (sorted rows)
+    uint16_t* hl = nullptr;      // [rows, I] h lo
+    float* y = nullptr;          // [rows, d] expert outputs at pair slots, shared rows after
     float* part = nullptr;       // [ksplit, maxT, E] router split-K partials
     int max_tiles = 0;
-    int ksplit = 1;
 };
 
 struct LayerState {
@@ -125,12 +123,12 @@ void prof_drain();
 int gu_blocks();
 int dn_blocks();
 int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg);
-int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
-                    const hfmoe_route_debug* dbg);
 int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                       const hfmoe_route_debug* dbg);
 int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s);
 // grouped_forward.hip
+int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                    const hfmoe_route_debug* dbg);
 int grouped_workspace_alloc();
 void grouped_workspace_free();
 // streamed.hip

@@ -5,17 +5,19 @@
 
 namespace hf {
 
-constexpr int kGemmTileRows = 128;  // M rows per grouped-GEMM tile
+constexpr int kGemmTileRows = 128;  // M rows per grouped-GEMM tile (256 at prefill sizes)
+constexpr int kGemmTileK = 64;      // K per pipeline stage (K % (64 * ksplit) == 0)
 
-enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2, EPI_COMBINE = 3 };
+enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 
 // Arguments of one grouped GEMM launch (see grouped_gemm.hip).
 struct GemmArgs {
-    int K;                      // reduction length (multiple of 32 * ksplit)
+    int K;                      // reduction length (multiple of 64 * ksplit)
     int N;                      // output columns (SWIGLU: intermediate rows per matrix)
     int n_tiles;                // ceil(N / columns per tile)
-    // M tiling: tile i covers rows [tile_row0[i], min(+128, group_end[tile_group[i]]))
-    const int* tile_group;      // null: one group, rows [0, rows_total) in 128-row tiles
+    int tile_rows;              // M rows per tile: 128 or 256
+    // M tiling: tile i covers rows [tile_row0[i], min(+tile_rows, group_end[tile_group[i]]))
+    const int* tile_group;      // null: one group, rows [0, rows_total) in tile_rows-row tiles
     const int* tile_row0;
     const int* ntiles_dev;      // device count of M tiles (null: m_tiles)
     int m_tiles;
@@ -33,25 +35,27 @@ struct GemmArgs {
     const uint16_t* b_fixed1;
     int b_ld;                   // B row stride in elements
     // epilogue operands
-    float* out_f32;             // PARTIAL [ksplit][rows][N]; SCATTER y rows; COMBINE out [T][N]
+    float* out_f32;             // PARTIAL [ksplit][rows][N]; SCATTER y rows
     uint16_t* h_hi;             // SWIGLU h [rows][N] hi / lo
     uint16_t* h_lo;
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
-    const float* comb_w;        // COMBINE: weights [T][comb_k]
-    const float* comb_y;        // COMBINE: y [T * comb_k][N]
-    int comb_k;
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
 };
 
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s);
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s);
+// out[t] = sum_r wts[t, r] * y[t*k + r] (+ y[shared_row0 + t] when shared_row0 >= 0); d % 4 == 0.
+hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d, int shared_row0,
+                          float* out, hipStream_t s);
 hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, const float* bias,
                                 float* logits, float2* scores, hipStream_t s);
 // Stable counting sort of the T*k (token, rank) pairs by expert plus the M-tile
-// list (tile_rows rows per tile) of the grouped GEMM.
-hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int* counts,
-                           int* offsets, int* perm, int* row_token, int* tile_expert,
+// list (tile_rows rows per tile) of the grouped GEMM.  With shared_rows > 0 a
+// group E of shared_rows rows (sorted rows T*k + t <- token t) follows the
+// experts: the shared expert multiplied in the same launches.
+hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
+                           int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
                            int* tile_row0, int* ntiles, hipStream_t s);
 
 }  // namespace hf

@@ -7,9 +7,11 @@
 
 namespace hf {
 
-// Timing hook: when set, the next launch records its own dispatch start and
-// end timestamps into these events (hipExtLaunchKernelGGL) and clears the hook,
-// so a measured duration is the kernel's alone, with no extra packets queued.
+// Timing hook: while set, launches record their dispatch timestamps into
+// these events (hipExtLaunchKernelGGL): the first launch of a timed section
+// records `start` (then cleared), every launch re-records `stop`, so a section
+// of one kernel measures that kernel alone, with no extra packets queued, and
+// a section of several spans the first one's start to the last one's end.
 struct LaunchTiming {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
@@ -19,10 +21,9 @@ extern LaunchTiming g_timing;
 template <typename... Params>
 inline hipError_t launch_exact(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem,
                                hipStream_t s, Params... args) {
-    if (g_timing.start) {
-        const LaunchTiming t = g_timing;
-        g_timing = LaunchTiming{};
-        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, t.start, t.stop, 0u, args...);
+    if (g_timing.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, g_timing.start, g_timing.stop, 0u, args...);
+        g_timing.start = nullptr;
     } else {
         hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
     }

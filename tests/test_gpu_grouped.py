@@ -57,6 +57,23 @@ def test_grouped_small(hf, T):
     r.free()
 
 
+def test_grouped_small_256_row_tiles(hf):
+    # 96+ rows per expert on average: the grouped GEMMs switch to 256-row tiles.
+    T, d = 1024, SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=58, T=T)
+    x = synth.make_x_dev(T, d, seed=58)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    counts = check_dispatch(res, SMALL["n_experts"])
+    assert counts.max() > 128  # some experts span more than one 128-row tile
+    check_selection(r, res, T)
+    for t in range(0, T, 64):
+        r.check_token(xh[t], res, t)
+    check_vs_decode(r, x, res, range(5, T, 97), d)
+    x.free()
+    r.free()
+
+
 def test_grouped_fp32_activations(hf):
     # Activations that are not BF16-valued take the hi + lo operand path.
     T, d = 24, SMALL["hidden"]
@@ -87,7 +104,7 @@ def test_grouped_without_shared_expert(hf):
 
 
 def test_tokenwise_fallback_untiled_shape(hf):
-    # hidden not a multiple of 32: the batch runs token by token on the decode kernels.
+    # hidden not a multiple of 64: the batch runs token by token on the decode kernels.
     dims = dict(hidden=1032, inter=520, n_experts=32, top_k=4)
     T = 3
     r = Run(dims, n_group=4, topk_group=2, seed=63, T=T)
