@@ -234,19 +234,22 @@ def run_grouped(args, workload: str) -> dict:
     d, I, E, S = shape.hidden, shape.inter, shape.n_experts, shape.n_shared
     layer_bytes = (U + S) * 3 * I * d * 2 + E * d * 2 + E * 4 + 2 * T * d * 4
     layer_flops = sum(f for _, f in algo.values())
-    if workload == "batched":
-        dom_name = max((n for n in algo if n in kernels), key=lambda n: kernels[n]["avg_us"])
-        dom = kernels[dom_name]
-        roof = {"bound": "hbm", "kernel": dom_name, "achieved": dom["gbs"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": traffic_from_profile(dom_name, "batched_t64_hbm_traffic.md")}
+    # Dominant kernel: the longest one.  Its roofline is HBM when its
+    # arithmetic intensity (algorithmic FLOP per algorithmic byte) is below the
+    # MI355X ridge point (2.5 PFLOP/s / 8 TB/s ~ 312), else MFMA.
+    dom_name = max((n for n in algo if n in kernels), key=lambda n: kernels[n]["avg_us"])
+    dom = kernels[dom_name]
+    ai = dom["algorithmic_flops"] / dom["algorithmic_bytes"]
+    summary = ("batched_t64" if workload == "batched" else "prefill_t4096") + "_hbm_traffic.md"
+    extra = {"arithmetic_intensity": round(ai, 1), "mfma_tflops": dom["tflops"],
+             "mfma_frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)}
+    if ai < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(dom_name, summary), **extra}
     else:
-        dom_name = "expert_gateup_gemm"
-        dom = kernels[dom_name]
-        roof = {"bound": "mfma", "kernel": dom_name, "achieved": dom["tflops"],
-                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": traffic_from_profile(dom_name, "prefill_t4096_hbm_traffic.md")}
+        roof = {"bound": "mfma", "kernel": dom_name, "achieved": dom["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": traffic_from_profile(dom_name, summary), **extra}
     res = {
         "value": T / sec,
         "ms_per_step": sec * 1e3,
@@ -305,7 +308,7 @@ def run_streamed(args) -> dict:
     prof, sec_prof = profiled_pass(step, args.steps)
     pcie = (p1.value - p0.value) / args.steps
     # Pinned host -> HBM copy rate of one layer's 8 selected experts, for the bound.
-    nbytes = shape.top_k * shape.expert_bytes()
+    nbytes = shape.top_k * shape.expert_bytes
     src = capi.PinnedBuffer(nbytes)
     dst = capi.DeviceBuffer(nbytes)
     capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
