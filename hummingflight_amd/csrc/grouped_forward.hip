@@ -34,14 +34,15 @@ static int router_ksplit(int T) {
     return best;
 }
 
-// Persistent grid: two 4-wave workgroups per CU (128-row tiles) or one 8-wave
+// Persistent grid: two 4-wave workgroups per CU (128-row tiles) or one
 // workgroup per CU (256-row tiles).
 static int gemm_blocks(int tile_rows) {
     return env_int("HFMOE_GEMM_BLOCKS", tile_rows == 256 ? g.num_cus : g.num_cus * 2);
 }
 
-// 256-row tiles once experts average 96+ rows (prefill): an expert's rows then
-// fit one tile and its weights stream through the memory system once.
+// 256 x 256 tiles once experts average 96+ rows (prefill): an expert's rows
+// then fit one tile, its weights stream through the memory system once, and
+// each activation row is requested once per 256 weight rows.
 static int expert_tile_rows(int T) {
     const Cfg& c = g.cfg;
     return (size_t)T * c.k >= (size_t)96 * c.E ? 256 : kGemmTileRows;
@@ -123,6 +124,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     r.K = c.d;
     r.N = c.E;
     r.tile_rows = kGemmTileRows;
+    r.tile_cols = 128;
     r.n_tiles = (c.E + 127) / 128;
     r.m_tiles = (T + kGemmTileRows - 1) / kGemmTileRows;
     r.rows_total = T;
@@ -152,7 +154,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.K = c.d;
     gu.N = c.I;
     gu.tile_rows = TR;
-    gu.n_tiles = (c.I + 63) / 64;
+    gu.tile_cols = TR;
+    gu.n_tiles = (c.I + TR / 2 - 1) / (TR / 2);
     gu.tile_group = w.tile_expert;
     gu.tile_row0 = w.tile_row0;
     gu.ntiles_dev = w.ntiles;
@@ -177,7 +180,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.K = c.I;
     dn.N = c.d;
     dn.tile_rows = TR;
-    dn.n_tiles = (c.d + 127) / 128;
+    dn.tile_cols = TR;
+    dn.n_tiles = (c.d + TR - 1) / TR;
     dn.tile_group = w.tile_expert;
     dn.tile_row0 = w.tile_row0;
     dn.ntiles_dev = w.ntiles;

@@ -331,6 +331,230 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
     }
 }
 
+// ---------------------------------------------------------------------------
+// Wide tiles for prefill: 256 (M) x 256 (N) x 64 (K), eight wavefronts, one
+// workgroup per CU.  Wavefront w owns tile rows [32w, 32w + 32) across all 256
+// columns, so each A fragment serves twice the columns of the 128-column tile
+// and the activation requests per FLOP halve -- at prefill sizes the CUs'
+// request bandwidth to L2, not HBM, bounds these GEMMs.  Same pipeline as
+// gemm_item: B by DMA into an LDS ring, A into registers, both D stages
+// ahead, explicit counter waits.
+constexpr int kWideRows = 256, kWideCols = 256;
+typedef uint16_t WStage[kWideCols * GBK];  // 32 KB: 256 weight rows x 64 k
+constexpr int kWideDepthHi = 2, kWideDepthLo = 1;
+constexpr size_t kWideRingBytes = sizeof(WStage) * (kWideDepthHi + 1);
+
+template <int EPI, bool USE_LO>
+__device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WStage* ring, int t, int wave) {
+    constexpr int BJ = 4;  // 1 KB weight DMAs per wave per stage (32 per stage)
+    constexpr int cols_per_tile = EPI == EPI_SWIGLU ? kWideCols / 2 : kWideCols;
+    constexpr int NA = USE_LO ? 8 : 4;  // A loads per wave per stage
+    constexpr int D = USE_LO ? kWideDepthLo : kWideDepthHi;
+    constexpr int RING = D + 1;
+    const int lane = t & 63;
+    const int fr = lane & 15;
+    const int fq = lane >> 4;
+    const int Kc = a.K / a.ksplit;
+    const int nk = Kc / GBK;
+
+    const int ks = item % a.ksplit;
+    const int rest = item / a.ksplit;
+    const int nt = rest % a.n_tiles;
+    const int mt = rest / a.n_tiles;
+    const int g = a.tile_group ? a.tile_group[mt] : 0;
+    const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * kWideRows;
+    const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
+    const int rows = min(kWideRows, row_end - row0);
+    const int n0 = nt * cols_per_tile;
+    const uint16_t* b0;
+    const uint16_t* b1 = nullptr;
+    if (a.b_tab) {
+        b0 = a.b_tab[3 * g + a.b_which];
+        if (EPI == EPI_SWIGLU) b1 = a.b_tab[3 * g + a.b_which + 1];
+    } else {
+        b0 = a.b_fixed0;
+        b1 = a.b_fixed1;
+    }
+    const int kbase = ks * Kc;
+    const int wrows = min(max(rows - 32 * wave, 0), 32);
+    const int nrb = (wrows + 15) >> 4;
+
+    // A rows of row blocks 0 and 1 (the lo half sits at a fixed offset from
+    // the hi half, so one pointer per row block serves both).
+    const uint16_t* ap[2];
+    const ptrdiff_t lo_off = USE_LO ? a.a_lo - a.a_hi : 0;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int lr = min(32 * wave + 16 * rb + fr, rows - 1);
+        const int gr = row0 + lr;
+        const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
+        ap[rb] = a.a_hi + src * a.K + kbase + fq * 8;
+    }
+    // Ring slot i (16 bytes) of a stage holds chunk (i & 7) ^ (row & 7) of tile
+    // row i >> 3; SWIGLU rows 0-127 are gate rows n0.., 128-255 the up rows.
+    // A wavefront's 32 slot rows lie in one half, so one base pointer plus
+    // 32-bit element offsets addresses them.
+    const uint16_t* bbase = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
+    uint32_t boff[BJ];
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+        const int i = (wave * BJ + j) * 64 + lane;
+        const int r = i >> 3;
+        const int c = (i & 7) ^ (r & 7);
+        int n = EPI == EPI_SWIGLU ? n0 + (r & 127) : n0 + r;
+        n = min(n, a.N - 1);
+        boff[j] = (uint32_t)((size_t)n * a.b_ld + kbase + c * 8);
+    }
+
+    f32x4_t acc[2][16];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 16; ++cb) acc[rb][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto issue_b = [&](int s) {
+        uint16_t* dst = ring[s % RING] + wave * BJ * 512;
+        s = min(s, nk - 1);
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) dma16(bbase + boff[j] + s * GBK, dst + j * 512);
+    };
+    typedef u32x4 AFrag[2][2][2];  // [hi/lo][row block][k half]
+    auto load_a = [&](AFrag& f, int s) {
+        s = min(s, nk - 1);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                f[0][rb][kh] = ld_global(ap[rb] + s * GBK + kh * 32);
+                if (USE_LO) f[1][rb][kh] = ld_global(ap[rb] + lo_off + s * GBK + kh * 32);
+            }
+    };
+    // Eight groups of four column blocks (k half kh = g >> 2, quarter g & 3);
+    // group g+1's B fragments are read while group g's MFMAs run (hi-only
+    // path; with the lo half the registers go to the lo A fragments instead).
+    constexpr int NB = USE_LO ? 1 : 2;
+    auto compute = [&](const uint16_t* bt, const AFrag& f) {
+        if (nrb == 0) return;
+        bf16x8_t bf[NB][4];
+        auto read_group = [&](int gi, bf16x8_t(&dst)[4]) {
+            const int kh = gi >> 2, cq = gi & 3;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 16 * (4 * cq + j) + fr;
+                const int c = (kh * 4 + fq) ^ (r & 7);
+                dst[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
+            }
+        };
+        if (NB == 2) read_group(0, bf[0]);
+#pragma unroll
+        for (int gi = 0; gi < 8; ++gi) {
+            if (NB == 1)
+                read_group(gi, bf[0]);
+            else if (gi + 1 < 8)
+                read_group(gi + 1, bf[(gi + 1) % NB]);
+            const int kh = gi >> 2, cq = gi & 3;
+            const bf16x8_t(&b)[4] = bf[gi % NB];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                if (rb == 1 && nrb < 2) break;
+                const bf16x8_t af = as_bf16x8(f[0][rb][kh]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[rb][4 * cq + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[j], acc[rb][4 * cq + j], 0, 0, 0);
+                if (USE_LO) {
+                    const bf16x8_t alf = as_bf16x8(f[1][rb][kh]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[rb][4 * cq + j] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(alf, b[j], acc[rb][4 * cq + j], 0, 0, 0);
+                }
+            }
+        }
+    };
+    auto step = [&](int s, const AFrag& cur, AFrag& ahead, auto tail) {
+        if constexpr (decltype(tail)::value)
+            wait_vmcnt<0>();
+        else
+            wait_vmcnt<(D - 1) * (NA + BJ)>();
+        lds_barrier();
+        load_a(ahead, s + D);
+        issue_b(s + D);
+        compute(ring[s % RING], cur);
+    };
+
+    AFrag A[RING];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        load_a(A[j], j);
+        issue_b(j);
+    }
+    int s = 0;
+    for (; s + RING <= nk; s += RING) {
+#pragma unroll
+        for (int u = 0; u < RING; ++u) step(s + u, A[u], A[(u + D) % RING], std::false_type{});
+    }
+#pragma unroll
+    for (int u = 0; u < RING - 1; ++u)
+        if (s + u < nk) step(s + u, A[u], A[(u + D) % RING], std::true_type{});
+
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        if (rb >= nrb) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rl_ = 32 * wave + 16 * rb + 4 * fq + q;
+            if (rl_ >= rows) continue;
+            const int gr = row0 + rl_;
+            if (EPI == EPI_SWIGLU) {
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) {
+                    const int col = n0 + 16 * cb + fr;
+                    if (col >= a.N) continue;
+                    const float gv = acc[rb][cb][q];
+                    const float uv = acc[rb][cb + 8][q];
+                    const float hv = gv / (1.0f + expf(-gv)) * uv;
+                    const uint16_t hb = f32_to_bf16(hv);
+                    const float hr = hv - __uint_as_float((uint32_t)hb << 16);
+                    a.h_hi[(size_t)gr * a.N + col] = hb;
+                    a.h_lo[(size_t)gr * a.N + col] = f32_to_bf16(hr);
+                }
+            } else {
+                float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
+                                                 : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
+#pragma unroll
+                for (int cb = 0; cb < 16; ++cb) {
+                    const int col = n0 + 16 * cb + fr;
+                    if (col < a.N) orow[col] = acc[rb][cb][q];
+                }
+            }
+        }
+    }
+}
+
+template <int EPI, bool LO>
+__global__ __launch_bounds__(512, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) WStage wring[];  // kWideRingBytes
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
+    const int total = m_tiles * a.n_tiles * a.ksplit;
+    const int nxcd = gridDim.x >= 8 ? 8 : 1;
+    const int xcd = blockIdx.x % nxcd;
+    const int per_xcd_blocks = (int)gridDim.x / nxcd + (xcd < (int)gridDim.x % nxcd ? 1 : 0);
+    const int local = blockIdx.x / nxcd;
+    const int chunk = (total + nxcd - 1) / nxcd;
+    const int item_begin = xcd * chunk;
+    const int item_end = min(total, item_begin + chunk);
+    const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
+    for (int item = item_begin + local; item < item_end; item += per_xcd_blocks) {
+        if (use_lo)
+            gemm_item_wide<EPI, LO>(a, item, wring, t, wave);
+        else
+            gemm_item_wide<EPI, false>(a, item, wring, t, wave);
+        __syncthreads();
+    }
+}
+
 // out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):
 // the weighted merge in rank order, then the shared expert (glm_forward.cpp:639-640, 658-660).
 __global__ void combine_kernel(const float* __restrict__ wts, const float* __restrict__ y, int T, int k,
@@ -403,9 +627,24 @@ static hipError_t launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
     return launch(grouped_gemm_kernel<EPI, LO, WAVES>, dim3(blocks), dim3(64 * WAVES), (uint32_t)kRingBytes, s, a);
 }
 
+template <int EPI, bool LO>
+static hipError_t launch_gemm_wide(const GemmArgs& a, int blocks, hipStream_t s) {
+    static bool raised = false;
+    if (!raised) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel<EPI, LO>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideRingBytes);
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    return launch(grouped_gemm_wide_kernel<EPI, LO>, dim3(blocks), dim3(512), (uint32_t)kWideRingBytes, s, a);
+}
+
 template <int EPI>
 static hipError_t launch_epi(const GemmArgs& a, int blocks, hipStream_t s) {
     const bool lo = a.a_lo != nullptr;
+    if (a.tile_rows == 256 && a.tile_cols == 256)
+        return lo ? launch_gemm_wide<EPI, true>(a, blocks, s) : launch_gemm_wide<EPI, false>(a, blocks, s);
+    if (a.tile_cols != 128) return hipErrorInvalidValue;
     if (a.tile_rows == 256)
         return lo ? launch_gemm<EPI, true, 8>(a, blocks, s) : launch_gemm<EPI, false, 8>(a, blocks, s);
     if (a.tile_rows == 128)

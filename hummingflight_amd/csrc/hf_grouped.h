@@ -14,8 +14,9 @@ enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 struct GemmArgs {
     int K;                      // reduction length (multiple of 64 * ksplit)
     int N;                      // output columns (SWIGLU: intermediate rows per matrix)
-    int n_tiles;                // ceil(N / columns per tile)
+    int n_tiles;                // ceil(N / output columns per tile); SWIGLU: tile_cols / 2 per tile
     int tile_rows;              // M rows per tile: 128 or 256
+    int tile_cols;              // B rows (weight rows) per tile: 128, or 256 with 256-row tiles
     // M tiling: tile i covers rows [tile_row0[i], min(+tile_rows, group_end[tile_group[i]]))
     const int* tile_group;      // null: one group, rows [0, rows_total) in tile_rows-row tiles
     const int* tile_row0;
