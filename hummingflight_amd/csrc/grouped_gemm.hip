@@ -139,35 +139,31 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
 
     // A fragment sources: lane row fr of row blocks 0 and 1, clamped to the
     // tile's last row (rows past it are loaded but never multiplied or stored).
+    // (the lo half sits at a fixed offset from the hi half: one pointer per row block)
     const uint16_t* ap[2];
-    const uint16_t* alp[2];
+    const ptrdiff_t lo_off = USE_LO ? a.a_lo - a.a_hi : 0;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
         const int lr = min(32 * wave + 16 * rb + fr, rows - 1);
         const int gr = row0 + lr;
         const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
         ap[rb] = a.a_hi + src * a.K + kbase + fq * 8;
-        alp[rb] = USE_LO ? a.a_lo + src * a.K + kbase + fq * 8 : nullptr;
     }
     // B DMA sources: wave w fills ring slots (BJ*w + j) * 64 + lane, j < BJ,
     // each 16 bytes: slot i holds chunk (i & 7) ^ (row & 7) of tile row i >> 3.
-    // Rows past N are clamped to row N-1 (their columns are never stored).
-    const uint16_t* bsrc[BJ];
+    // Rows past N are clamped to row N-1 (their columns are never stored).  A
+    // wavefront's slot rows lie in one half (gate or up), so one base pointer
+    // plus 32-bit element offsets addresses them.
+    const uint16_t* bbase = (EPI == EPI_SWIGLU && wave >= WAVES / 2) ? b1 : b0;
+    uint32_t boff[BJ];
 #pragma unroll
     for (int j = 0; j < BJ; ++j) {
         const int i = (wave * BJ + j) * 64 + lane;
         const int r = i >> 3;
         const int c = (i & 7) ^ (r & 7);
-        const uint16_t* base = b0;
-        int n;
-        if (EPI == EPI_SWIGLU) {
-            n = n0 + (r & 63);
-            if (r >= 64) base = b1;
-        } else {
-            n = n0 + r;
-        }
+        int n = EPI == EPI_SWIGLU ? n0 + (r & 63) : n0 + r;
         n = min(n, a.N - 1);
-        bsrc[j] = base + (size_t)n * a.b_ld + kbase + c * 8;
+        boff[j] = (uint32_t)((size_t)n * a.b_ld + kbase + c * 8);
     }
 
     f32x4_t acc[2][8];
@@ -182,7 +178,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
         uint16_t* dst = ring[s % RING] + wave * BJ * 512;
         s = min(s, nk - 1);
 #pragma unroll
-        for (int j = 0; j < BJ; ++j) dma16(bsrc[j] + s * GBK, dst + j * 512);
+        for (int j = 0; j < BJ; ++j) dma16(bbase + boff[j] + s * GBK, dst + j * 512);
     };
     typedef u32x4 AFrag[2][2][2];  // [hi/lo][row block][k half]
     auto load_a = [&](AFrag& f, int s) {
@@ -192,15 +188,16 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) {
                 f[0][rb][kh] = ld_global(ap[rb] + s * GBK + kh * 32);
-                if (USE_LO) f[1][rb][kh] = ld_global(alp[rb] + s * GBK + kh * 32);
+                if (USE_LO) f[1][rb][kh] = ld_global(ap[rb] + lo_off + s * GBK + kh * 32);
             }
     };
     // Four groups of four column blocks (k half kh = g >> 1, column half
     // ch = g & 1); the B fragments of group g+1 are read from LDS while the
     // MFMAs of group g run.
+    constexpr int NB = 2;  // B fragment sets
     auto compute = [&](const uint16_t* bt, const AFrag& f) {
         if (nrb == 0) return;
-        bf16x8_t bf[2][4];
+        bf16x8_t bf[NB][4];
         auto read_group = [&](int g, bf16x8_t(&dst)[4]) {
             const int kh = g >> 1, ch = g & 1;
 #pragma unroll
@@ -210,12 +207,15 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
                 dst[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
             }
         };
-        read_group(0, bf[0]);
+        if (NB == 2) read_group(0, bf[0]);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            if (g + 1 < 4) read_group(g + 1, bf[(g + 1) & 1]);
+            if (NB == 1)
+                read_group(g, bf[0]);
+            else if (g + 1 < 4)
+                read_group(g + 1, bf[(g + 1) % NB]);
             const int kh = g >> 1, ch = g & 1;
-            const bf16x8_t(&b)[4] = bf[g & 1];
+            const bf16x8_t(&b)[4] = bf[g % NB];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 if (rb == 1 && nrb < 2) break;
