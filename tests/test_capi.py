@@ -66,3 +66,17 @@ def test_calls_before_init_fail_loudly():
     assert L.hfmoe_moe_forward(0, None, 1, None, None) == capi.ERR_NOT_INITIALIZED
     assert L.hfmoe_expert_stage(0, 0, None, 64, 32) != capi.OK
     assert L.hfmoe_device_memory_mb() == 0
+
+
+def test_engine_shim_builds_and_fails_cleanly_without_device():
+    """The C++ caller compiles against include/hfmoe.h, links libhfmoe.so and,
+    with no usable device, stops with the start-up error (exit code 2)."""
+    shim_dir = os.path.join(ROOT, "tests", "engine_shim")
+    subprocess.run(["make", "-s", "-C", shim_dir], check=True)
+    r = subprocess.run([os.path.join(shim_dir, "engine_shim"), "1", "1"], capture_output=True, text=True,
+                       timeout=120)
+    if r.returncode == 2:
+        assert "no usable device" in r.stderr
+    else:  # a machine with a GPU: one line of hidden-size hex words
+        assert r.returncode == 0, r.stderr
+        assert len(r.stdout.split()) == 2048

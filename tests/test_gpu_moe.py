@@ -190,3 +190,26 @@ def test_mlp_block_chain(hf):
     for L in layers:
         L.free()
     h.free()
+
+
+def test_engine_shim_cpp_caller(hf):
+    # The C++ engine-side shim (tests/engine_shim) through the moeLayer host
+    # contract: same seeded layer as the oracle's, two tokens.
+    import os
+    import subprocess
+    shim = os.path.join(os.path.dirname(os.path.abspath(__file__)), "engine_shim", "engine_shim")
+    if not os.path.exists(shim):
+        pytest.skip("engine shim not built (python __graft_entry__.py builds it)")
+    capi.load().hfmoe_shutdown()  # the shim is its own process with its own device context
+    seed, T = 77, 2
+    r = subprocess.run([shim, str(seed), str(T)], capture_output=True, text=True, timeout=120)
+    capi.call("hfmoe_init", 0)
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.strip().splitlines()
+    assert len(lines) == T
+    ref = O.SyntheticLayer(O.LayerSpec(n_group=8, topk_group=4, seed=seed, **SMALL))
+    xs = O.make_x(T, SMALL["hidden"], seed)
+    for t in range(T):
+        got = np.array([int(v, 16) for v in lines[t].split()], np.uint32).view(np.float32)
+        out, _, _, _ = ref.forward(xs[t])
+        assert_close(got, out, f"engine shim token {t}")
