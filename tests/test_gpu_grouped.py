@@ -176,3 +176,29 @@ def test_grouped_repeat_is_deterministic(hf):
     assert np.array_equal(c["out"], a["out"][:5])
     x.free()
     r.free()
+
+
+EDGE = [
+    # (name, dims, routing kwargs, n_group, topk_group, n_shared, T)
+    ("one_k_stage", dict(hidden=64, inter=64, n_experts=16, top_k=4), {}, 4, 2, 1, 9),
+    ("top1_flat", dict(hidden=512, inter=256, n_experts=16, top_k=1), {}, 1, 1, 1, 33),
+    ("unnormalised_scale1", dict(hidden=512, inter=256, n_experts=32, top_k=4),
+     dict(norm_topk_prob=False, routed_scaling_factor=1.0), 4, 2, 1, 20),
+    ("experts_not_multiple_of_128", dict(hidden=768, inter=320, n_experts=96, top_k=6), {}, 8, 3, 1, 40),
+    ("flat_256_experts", dict(hidden=1024, inter=512, n_experts=256, top_k=8), {}, 1, 1, 0, 48),
+]
+
+
+@pytest.mark.parametrize("name,dims,routing,n_group,topk_group,n_shared,T", EDGE, ids=[e[0] for e in EDGE])
+def test_grouped_edge_shapes(hf, name, dims, routing, n_group, topk_group, n_shared, T):
+    r = Run(dims, n_group=n_group, topk_group=topk_group, seed=70, T=T, n_shared=n_shared, **routing)
+    x = synth.make_x_dev(T, dims["hidden"], seed=70)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * dims["hidden"]).reshape(T, -1)
+    check_dispatch(res, dims["n_experts"])
+    for t in range(T):
+        r.check_token(xh[t], res, t)
+    # The decode kernels agree for the same tokens (T = 1 calls).
+    check_vs_decode(r, x, res, range(0, T, max(1, T // 4)), dims["hidden"])
+    x.free()
+    r.free()
