@@ -9,7 +9,7 @@
 #include <utility>
 #include <vector>
 
-#include "../../include/hfmoe.h"
+#include "hfmoe.h"
 #include "hf_kernels.h"
 
 namespace hf {
