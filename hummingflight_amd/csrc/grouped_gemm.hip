@@ -24,9 +24,8 @@
 //     (global_load_lds_dwordx4) with no register staging, and A fragments
 //     straight into registers (L2-resident activations, row-gathered through
 //     a_rowmap); both are fetched 2-4 K stages ahead of the one multiplied;
-//   * persistent workgroups walk a contiguous range of (m-tile, n-tile) items
-//     per XCD, n fastest, so an M tile's activations and the B slices shared
-//     by an expert's M tiles are reused within that XCD's L2.
+//   * persistent workgroups walk per-XCD item lists, n fastest, so an M
+//     tile's activations are reused within that XCD's L2 (item_range).
 //
 // Epilogues:
 //   PARTIAL  split-K partial sums (router logits; reduced in fixed order later)
@@ -90,6 +89,46 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// The items (m-tile, n-tile, k-split) a persistent workgroup walks.  The
+// hardware deals workgroups to the 8 XCDs round-robin, so blockIdx.x % 8 is
+// the XCD, and each XCD takes a contiguous range of items (an M tile's N
+// tiles, which share its activation rows, run side by side in one L2).
+// DEAL_M (256-row prefill tiles, at least one M tile per XCD): whole M tiles
+// are dealt to the XCDs round-robin instead, which keeps the first property
+// and spreads runs of heavy tiles -- the shared expert's full 256-row tiles
+// sit together at the end of the list, with twice the MFMA work of a routed
+// expert's ~128 rows -- over all XCDs rather than the last one.
+struct ItemRange {
+    int begin, end, stride;  // local item indices begin, begin + stride, ... < end
+    int xcd, nxcd, per_m;    // per_m = n_tiles * ksplit items per M tile
+    bool by_mtile;
+    __device__ __forceinline__ int item(int li) const {
+        return by_mtile ? (xcd + nxcd * (li / per_m)) * per_m + li % per_m : li;
+    }
+};
+
+template <bool DEAL_M>
+__device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) {
+    ItemRange r;
+    r.nxcd = gridDim.x >= 8 ? 8 : 1;
+    r.xcd = blockIdx.x % r.nxcd;
+    r.stride = (int)gridDim.x / r.nxcd + (r.xcd < (int)gridDim.x % r.nxcd ? 1 : 0);
+    r.per_m = a.n_tiles * a.ksplit;
+    r.by_mtile = DEAL_M && m_tiles >= r.nxcd;
+    const int local = blockIdx.x / r.nxcd;
+    if (r.by_mtile) {
+        const int m_local = (m_tiles - r.xcd + r.nxcd - 1) / r.nxcd;
+        r.begin = local;
+        r.end = m_local * r.per_m;
+    } else {
+        const int total = m_tiles * r.per_m;
+        const int chunk = (total + r.nxcd - 1) / r.nxcd;
+        r.begin = r.xcd * chunk + local;
+        r.end = min(total, r.xcd * chunk + chunk);
+    }
+    return r;
 }
 
 // One (m-tile, n-tile, k-split) item.  USE_LO: multiply the A lo half too.
@@ -310,19 +349,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar branches
 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
-    const int total = m_tiles * a.n_tiles * a.ksplit;
-    // Contiguous range of items per XCD (blocks are dealt to XCDs round-robin).
-    const int nxcd = gridDim.x >= 8 ? 8 : 1;
-    const int xcd = blockIdx.x % nxcd;
-    const int per_xcd_blocks = (int)gridDim.x / nxcd + (xcd < (int)gridDim.x % nxcd ? 1 : 0);
-    const int local = blockIdx.x / nxcd;
-    const int chunk = (total + nxcd - 1) / nxcd;
-    const int item_begin = xcd * chunk;
-    const int item_end = min(total, item_begin + chunk);
+    const ItemRange r = item_range<false>(a, m_tiles);
     // The lo half is multiplied only when present (x that is BF16-valued has none).
     const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
 
-    for (int item = item_begin + local; item < item_end; item += per_xcd_blocks) {
+    for (int li = r.begin; li < r.end; li += r.stride) {
+        const int item = r.item(li);
         if (use_lo)
             gemm_item<EPI, LO, WAVES>(a, item, ring, t, wave);
         else
@@ -537,16 +569,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
-    const int total = m_tiles * a.n_tiles * a.ksplit;
-    const int nxcd = gridDim.x >= 8 ? 8 : 1;
-    const int xcd = blockIdx.x % nxcd;
-    const int per_xcd_blocks = (int)gridDim.x / nxcd + (xcd < (int)gridDim.x % nxcd ? 1 : 0);
-    const int local = blockIdx.x / nxcd;
-    const int chunk = (total + nxcd - 1) / nxcd;
-    const int item_begin = xcd * chunk;
-    const int item_end = min(total, item_begin + chunk);
+    const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
-    for (int item = item_begin + local; item < item_end; item += per_xcd_blocks) {
+    for (int li = r.begin; li < r.end; li += r.stride) {
+        const int item = r.item(li);
         if (use_lo)
             gemm_item_wide<EPI, LO>(a, item, wring, t, wave);
         else
