@@ -131,6 +131,59 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
     return r;
 }
 
+// Stores one lane's share of a finished tile row gr: acc[cb][q] is output
+// column col0 + 16*cb + q (q = 0..3).  SWIGLU: blocks [0, NCB/2) are gate and
+// [NCB/2, NCB) the matching up columns; writes h = silu(g) * u as BF16 hi/lo
+// (glm_forward.cpp:444-446), 8 bytes each.  PARTIAL / SCATTER: 16-byte FP32
+// stores (row stride N is a multiple of 4 whenever N is a multiple of 64;
+// a ragged router width falls back to single floats).
+template <int EPI, int NCB>
+__device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t (&acc)[NCB], int gr, int col0,
+                                               int ks) {
+    if (EPI == EPI_SWIGLU) {
+        uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
+        uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
+#pragma unroll
+        for (int cb = 0; cb < NCB / 2; ++cb) {
+            const int col = col0 + 16 * cb;
+            if (col >= a.N) continue;  // N is a multiple of 64: 4 columns all in or all out
+            uint32_t hw[2], lw[2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float gv = acc[cb][q];
+                const float uv = acc[cb + NCB / 2][q];
+                const float hv = gv / (1.0f + expf(-gv)) * uv;
+                const uint32_t hb = f32_to_bf16(hv);
+                const uint32_t lb = f32_to_bf16(hv - __uint_as_float(hb << 16));
+                if (q & 1) {
+                    hw[q >> 1] |= hb << 16;
+                    lw[q >> 1] |= lb << 16;
+                } else {
+                    hw[q >> 1] = hb;
+                    lw[q >> 1] = lb;
+                }
+            }
+            *reinterpret_cast<uint2*>(hrow + col) = make_uint2(hw[0], hw[1]);
+            *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
+        }
+    } else {
+        float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
+                                         : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
+        const bool vec = (a.N & 3) == 0;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            const int col = col0 + 16 * cb;
+            if (vec && col + 3 < a.N) {
+                *reinterpret_cast<f32x4_t*>(orow + col) = acc[cb];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (col + q < a.N) orow[col + q] = acc[cb][q];
+            }
+        }
+    }
+}
+
 // One (m-tile, n-tile, k-split) item.  USE_LO: multiply the A lo half too.
 //
 // Pipeline per K stage s (64 k), prefetch distance D: every wave waits until
@@ -261,13 +314,13 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
                 const bf16x8_t af = as_bf16x8(f[0][rb][kh]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[rb][4 * ch + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[j], acc[rb][4 * ch + j], 0, 0, 0);
+                    acc[rb][4 * ch + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], af, acc[rb][4 * ch + j], 0, 0, 0);
                 if (USE_LO) {
                     const bf16x8_t alf = as_bf16x8(f[1][rb][kh]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         acc[rb][4 * ch + j] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(alf, b[j], acc[rb][4 * ch + j], 0, 0, 0);
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], alf, acc[rb][4 * ch + j], 0, 0, 0);
                 }
             }
         }
@@ -304,38 +357,14 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
     for (int u = 0; u < RING - 1; ++u)
         if (s + u < nk) step(s + u, A[u], A[(u + D) % RING], std::true_type{});
 
-    // Epilogue: lane holds D[4*fq + q][fr] of each 16 x 16 block.
+    // Epilogue.  The MFMAs take the weight fragment as their A operand, so a
+    // lane holds output columns 16*cb + 4*fq + q (q = 0..3, consecutive) of
+    // tile row 32*wave + 16*rb + fr: each store writes 4 adjacent columns.
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
         if (rb >= nrb) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int rl_ = 32 * wave + 16 * rb + 4 * fq + q;
-            if (rl_ >= rows) continue;
-            const int gr = row0 + rl_;
-            if (EPI == EPI_SWIGLU) {
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
-                    const int col = n0 + 16 * cb + fr;
-                    if (col >= a.N) continue;
-                    const float gv = acc[rb][cb][q];
-                    const float uv = acc[rb][cb + 4][q];
-                    const float hv = gv / (1.0f + expf(-gv)) * uv;
-                    const uint16_t hb = f32_to_bf16(hv);
-                    const float hr = hv - __uint_as_float((uint32_t)hb << 16);
-                    a.h_hi[(size_t)gr * a.N + col] = hb;
-                    a.h_lo[(size_t)gr * a.N + col] = f32_to_bf16(hr);
-                }
-            } else {
-                float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
-                                                 : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) {
-                    const int col = n0 + 16 * cb + fr;
-                    if (col < a.N) orow[col] = acc[rb][cb][q];
-                }
-            }
-        }
+        const int rl = 32 * wave + 16 * rb + fr;
+        if (rl < rows) store_tile_row<EPI, 8>(a, acc[rb], row0 + rl, n0 + 4 * fq, ks);
     }
 }
 
@@ -492,13 +521,13 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WSta
                 const bf16x8_t af = as_bf16x8(f[0][rb][kh]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[rb][4 * cq + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, b[j], acc[rb][4 * cq + j], 0, 0, 0);
+                    acc[rb][4 * cq + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], af, acc[rb][4 * cq + j], 0, 0, 0);
                 if (USE_LO) {
                     const bf16x8_t alf = as_bf16x8(f[1][rb][kh]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         acc[rb][4 * cq + j] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(alf, b[j], acc[rb][4 * cq + j], 0, 0, 0);
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], alf, acc[rb][4 * cq + j], 0, 0, 0);
                 }
             }
         }
@@ -529,37 +558,12 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WSta
     for (int u = 0; u < RING - 1; ++u)
         if (s + u < nk) step(s + u, A[u], A[(u + D) % RING], std::true_type{});
 
+    // Epilogue: as in gemm_item, 4 adjacent output columns per store.
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
         if (rb >= nrb) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int rl_ = 32 * wave + 16 * rb + 4 * fq + q;
-            if (rl_ >= rows) continue;
-            const int gr = row0 + rl_;
-            if (EPI == EPI_SWIGLU) {
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) {
-                    const int col = n0 + 16 * cb + fr;
-                    if (col >= a.N) continue;
-                    const float gv = acc[rb][cb][q];
-                    const float uv = acc[rb][cb + 8][q];
-                    const float hv = gv / (1.0f + expf(-gv)) * uv;
-                    const uint16_t hb = f32_to_bf16(hv);
-                    const float hr = hv - __uint_as_float((uint32_t)hb << 16);
-                    a.h_hi[(size_t)gr * a.N + col] = hb;
-                    a.h_lo[(size_t)gr * a.N + col] = f32_to_bf16(hr);
-                }
-            } else {
-                float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
-                                                 : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
-#pragma unroll
-                for (int cb = 0; cb < 16; ++cb) {
-                    const int col = n0 + 16 * cb + fr;
-                    if (col < a.N) orow[col] = acc[rb][cb][q];
-                }
-            }
-        }
+        const int rl = 32 * wave + 16 * rb + fr;
+        if (rl < rows) store_tile_row<EPI, 16>(a, acc[rb], row0 + rl, n0 + 4 * fq, ks);
     }
 }
 
