@@ -53,6 +53,22 @@ class KernelStat(C.Structure):
     _fields_ = [("name", C.c_char * 32), ("launches", C.c_int64), ("total_ms", C.c_double)]
 
 
+class StreamOptions(C.Structure):
+    _fields_ = [("prefetch_next_layer", C.c_int32), ("ema_predictor", C.c_int32),
+                ("ema_alpha", C.c_float), ("overlap_floor", C.c_float), ("overlap_alpha", C.c_float),
+                ("reserved", C.c_int32 * 3)]
+
+
+class StreamCounters(C.Structure):
+    _fields_ = [("lookups", C.c_uint64), ("hits", C.c_uint64), ("misses", C.c_uint64),
+                ("pred_staged", C.c_uint64), ("pred_consumed", C.c_uint64), ("pred_wasted", C.c_uint64),
+                ("pred_resident", C.c_uint64), ("copies", C.c_uint64), ("slots", C.c_int32),
+                ("reserved", C.c_int32)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+
+
 # (name, restype, argtypes) for every entry point of include/hfmoe.h.
 _SIGS = [
     ("hfmoe_init", C.c_int, [C.c_int]),
@@ -90,6 +106,10 @@ _SIGS = [
     ("hfmoe_profile_enable", C.c_int, [C.c_int]),
     ("hfmoe_profile_read", C.c_int, [C.POINTER(KernelStat), C.c_int, C.POINTER(C.c_int)]),
     ("hfmoe_profile_reset", C.c_int, []),
+    ("hfmoe_stream_set_options", C.c_int, [C.POINTER(StreamOptions)]),
+    ("hfmoe_stream_get_options", C.c_int, [C.POINTER(StreamOptions)]),
+    ("hfmoe_stream_read_counters", C.c_int, [C.POINTER(StreamCounters)]),
+    ("hfmoe_stream_reset", C.c_int, []),
     ("hfmoe_stats", C.c_int, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
 ]
 

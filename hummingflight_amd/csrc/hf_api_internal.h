@@ -9,6 +9,7 @@
 #include <utility>
 #include <vector>
 
+#include "expert_stream_policy.h"
 #include "hfmoe.h"
 #include "hf_kernels.h"
 
@@ -61,16 +62,15 @@ struct Pending {
 };
 
 // Staging pool of the streamed-expert path: HBM slots that receive selected
-// experts from pinned host RAM on the copy stream.
+// (and predicted) experts from pinned host RAM on the copy stream.  Which
+// slot holds what is decided by `policy`.
 struct StreamPool {
     int slots = 0;
     size_t slot_bytes = 0;
     uint16_t* base = nullptr;
     std::vector<hipEvent_t> copied;   // per slot: H2D done (copy stream)
     std::vector<hipEvent_t> consumed; // per slot: last kernel reading it done
-    std::vector<uint64_t> key;        // (layer << 32 | expert) resident in slot, or ~0
-    std::vector<uint64_t> last_use;
-    uint64_t clock = 0;
+    ExpertStreamPolicy policy;
     int* idx_host = nullptr;          // pinned [k] selected experts readback
     float* w_host = nullptr;
     const uint16_t** etab_host = nullptr;  // pinned [3*k] slot pointers for the table
@@ -78,7 +78,6 @@ struct StreamPool {
     int* iota_dev = nullptr;               // device [k] = 0..k-1 (slot order)
     float* shared_out = nullptr;           // device [d] shared-expert output
     hipEvent_t routed = nullptr;
-    uint64_t hits = 0, misses = 0;
 };
 
 struct State {
@@ -97,6 +96,7 @@ struct State {
     Workspace ws;
     GroupedWorkspace gws;
     StreamPool pool;
+    StreamPolicyOptions stream_opt;   // kept across hfmoe_configure
     // profiling / telemetry
     bool prof_on = false;
     std::vector<Pending> pending;

@@ -3,15 +3,19 @@
 // The on-device counterpart of the reference's scheduler + GPU staging window
 // (Scheduler::getExpertPtr scheduler.cpp:646-741 feeding gpuExpertStage,
 // cuda_backend.cpp:395-428, from moeLayer glm_forward.cpp:562-602): only the k
-// experts the router selects cross PCIe.
+// experts the router selects cross PCIe, into an HBM slot pool that caches
+// them (LRU) and, once a layer has routed, receives the experts predicted for
+// the next layer ahead of time (Scheduler::onLayerRouterDone,
+// scheduler.cpp:238-388).  Slot and prediction decisions: expert_stream_policy.h.
 //
 // Per call (T = 1), on the caller's stream s and the library's copy stream:
 //   s:    router -> D2H of the k selected ids (pinned) -> event `routed`
 //   s:    shared expert gate/up + down into shared_out (overlaps the copies)
-//   host: wait `routed`; for each selected expert look up the HBM slot pool
-//         (LRU keyed by layer and expert): a hit reuses the slot, a miss
-//         queues three hipMemcpyAsync (gate, up, down) on the copy stream
-//         after the slot's previous reader finished, then records `copied`
+//   host: wait `routed`; look up each selected expert: a resident slot (or one
+//         already being filled by a copy-ahead) is reused, a miss queues three
+//         hipMemcpyAsync (gate, up, down) on the copy stream after the slot's
+//         previous reader finished, then records `copied`
+//   copy: then the copies of the next layer's predicted experts
 //   s:    wait every used slot's `copied`, upload the 3k slot pointers, run
 //         the routed gate/up and down GEMVs with out = routed sum + shared_out,
 //         record each slot's `consumed`.
@@ -44,19 +48,20 @@ static int pool_init() {
     const Cfg& c = g.cfg;
     P.slot_bytes = (size_t)6 * c.d * c.I;
     // Slots: the VRAM budget (AdaptiveConfig::vramBudgetBytes) when given,
-    // else two layers' worth of selected experts; never fewer than k.
+    // else two layers' worth of selected experts; never fewer than 2k (one
+    // layer's selection plus the next layer's copy-ahead).
     int slots = 2 * c.k;
-    if (g.vram_budget) slots = (int)(g.vram_budget / P.slot_bytes);
-    if (slots < c.k) slots = c.k;
+    if (g.vram_budget) slots = (int)std::min<uint64_t>(g.vram_budget / P.slot_bytes, 1 << 20);
+    if (slots < 2 * c.k) slots = 2 * c.k;
     hipError_t e = hipMalloc(&P.base, P.slot_bytes * (size_t)slots);
     if (e != hipSuccess)
         return fail(HFMOE_ERR_OUT_OF_MEMORY, "expert staging pool (%d x %zu bytes): %s", slots,
                     P.slot_bytes, hipGetErrorString(e));
     P.slots = slots;
+    P.policy.reset(slots);
+    P.policy.opt = g.stream_opt;
     P.copied.assign(slots, nullptr);
     P.consumed.assign(slots, nullptr);
-    P.key.assign(slots, ~0ull);
-    P.last_use.assign(slots, 0);
     for (int i = 0; i < slots && e == hipSuccess; ++i) {
         e = hipEventCreateWithFlags(&P.copied[i], hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&P.consumed[i], hipEventDisableTiming);
@@ -77,6 +82,22 @@ static int pool_init() {
         stream_pool_release();
         return fail_hip(e, "expert staging pool setup");
     }
+    return HFMOE_OK;
+}
+
+// Queues expert eid's [gate | up | down] (host) into slot on the copy stream,
+// after the last kernel that read the slot.
+static int copy_expert(const LayerState& L, int eid, int slot) {
+    StreamPool& P = g.pool;
+    const size_t proj = (size_t)g.cfg.I * g.cfg.d;
+    uint16_t* dst = P.base + (size_t)slot * (P.slot_bytes / 2);
+    hipError_t e = hipStreamWaitEvent(g.copy_stream, P.consumed[slot], 0);
+    for (int q = 0; q < 3 && e == hipSuccess; ++q)
+        e = hipMemcpyAsync(dst + q * proj, L.host_experts[3 * eid + q], proj * 2, hipMemcpyHostToDevice,
+                           g.copy_stream);
+    if (e == hipSuccess) e = hipEventRecord(P.copied[slot], g.copy_stream);
+    if (e != hipSuccess) return fail_hip(e, "expert H2D");
+    g.pcie_bytes += 3 * proj * 2;
     return HFMOE_OK;
 }
 
@@ -121,45 +142,18 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
     e = hipEventSynchronize(P.routed);
     if (e != hipSuccess) return fail_hip(e, "wait for routing");
 
-    int used[kMaxTopK];
+    int used[2 * kMaxTopK];
     const size_t proj = (size_t)c.I * c.d;
     for (int r = 0; r < c.k; ++r) {
         const int eid = P.idx_host[r];
         if (eid < 0 || eid >= c.E) return fail(HFMOE_ERR_HIP, "router produced expert id %d", eid);
-        const uint64_t key = ((uint64_t)(uint32_t)layer << 32) | (uint32_t)eid;
-        int slot = -1;
-        for (int i = 0; i < P.slots; ++i)
-            if (P.key[i] == key) slot = i;
-        if (slot >= 0) {
-            ++P.hits;
-        } else {
-            // LRU victim among slots this call has not claimed.
-            uint64_t oldest = ~0ull;
-            for (int i = 0; i < P.slots; ++i) {
-                bool taken = false;
-                for (int q = 0; q < r; ++q) taken |= (used[q] == i);
-                if (taken) continue;
-                if (P.key[i] == ~0ull) {
-                    slot = i;
-                    break;
-                }
-                if (P.last_use[i] < oldest) {
-                    oldest = P.last_use[i];
-                    slot = i;
-                }
-            }
-            uint16_t* dst = P.base + (size_t)slot * (P.slot_bytes / 2);
-            e = hipStreamWaitEvent(g.copy_stream, P.consumed[slot], 0);
-            for (int q = 0; q < 3 && e == hipSuccess; ++q)
-                e = hipMemcpyAsync(dst + q * proj, L.host_experts[3 * eid + q], proj * 2,
-                                   hipMemcpyHostToDevice, g.copy_stream);
-            if (e == hipSuccess) e = hipEventRecord(P.copied[slot], g.copy_stream);
-            if (e != hipSuccess) return fail_hip(e, "expert H2D");
-            P.key[slot] = key;
-            ++P.misses;
-            g.pcie_bytes += 3 * proj * 2;
+        bool copy = false;
+        const int slot = P.policy.lookup(layer, eid, used, r, &copy);
+        if (slot < 0) return fail(HFMOE_ERR_HIP, "expert slot pool exhausted");
+        if (copy) {
+            int rc2 = copy_expert(L, eid, slot);
+            if (rc2) return rc2;
         }
-        P.last_use[slot] = ++P.clock;
         used[r] = slot;
         const uint16_t* base = P.base + (size_t)slot * (P.slot_bytes / 2);
         P.etab_host[3 * r] = base;
@@ -167,6 +161,21 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
         P.etab_host[3 * r + 2] = base + 2 * proj;
         e = hipStreamWaitEvent(s, P.copied[slot], 0);
         if (e != hipSuccess) return fail_hip(e, "wait for expert H2D");
+    }
+    // Copy-ahead of the next layer's predicted experts, queued behind this
+    // layer's copies; slots this call uses (and earlier copy-aheads of the
+    // batch) are not victims.
+    auto nx = g.layers.find(layer + 1);
+    const bool next_streamed = nx != g.layers.end() && nx->second.location == HFMOE_EXPERTS_HOST_PINNED;
+    const std::vector<int> guess = P.policy.route_done(layer, P.idx_host, c.k, next_streamed);
+    int nclaimed = c.k;
+    for (int eid : guess) {
+        if (eid < 0 || eid >= c.E || nclaimed >= 2 * kMaxTopK) continue;
+        const int slot = P.policy.stage(layer + 1, eid, used, nclaimed);
+        if (slot < 0) continue;
+        int rc2 = copy_expert(nx->second, eid, slot);
+        if (rc2) return rc2;
+        used[nclaimed++] = slot;
     }
     e = hipMemcpyAsync(P.etab_dev, P.etab_host, sizeof(void*) * 3 * c.k, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return fail_hip(e, "slot table upload");
@@ -199,3 +208,68 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
 }
 
 }  // namespace hf
+
+using namespace hf;
+
+extern "C" {
+
+int hfmoe_stream_set_options(const hfmoe_stream_options* o) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!o) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null options");
+    if (!(o->ema_alpha > 0.0f && o->ema_alpha <= 1.0f) || !(o->overlap_alpha >= 0.0f && o->overlap_alpha <= 1.0f))
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "ema_alpha must be in (0, 1] and overlap_alpha in [0, 1]");
+    StreamPolicyOptions& so = g.stream_opt;
+    so.prefetch = o->prefetch_next_layer != 0;
+    so.ema_predictor = o->ema_predictor != 0;
+    so.ema_alpha = o->ema_alpha;
+    so.overlap_floor = o->overlap_floor;
+    so.overlap_alpha = o->overlap_alpha;
+    g.pool.policy.opt = so;
+    return HFMOE_OK;
+}
+
+int hfmoe_stream_get_options(hfmoe_stream_options* o) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!o) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null options");
+    *o = hfmoe_stream_options{};
+    const StreamPolicyOptions& so = g.stream_opt;
+    o->prefetch_next_layer = so.prefetch;
+    o->ema_predictor = so.ema_predictor;
+    o->ema_alpha = so.ema_alpha;
+    o->overlap_floor = so.overlap_floor;
+    o->overlap_alpha = so.overlap_alpha;
+    return HFMOE_OK;
+}
+
+int hfmoe_stream_read_counters(hfmoe_stream_counters* out) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!out) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null counters");
+    const StreamPolicyCounters& n = g.pool.policy.n;
+    *out = hfmoe_stream_counters{};
+    out->lookups = n.lookups;
+    out->hits = n.hits;
+    out->misses = n.misses;
+    out->pred_staged = n.pred_staged;
+    out->pred_consumed = n.pred_consumed;
+    out->pred_wasted = n.pred_wasted;
+    out->pred_resident = n.pred_resident;
+    out->copies = n.copies;
+    out->slots = g.pool.slots;
+    return HFMOE_OK;
+}
+
+int hfmoe_stream_reset(void) {
+    int rc = require_init();
+    if (rc) return rc;
+    // Host bookkeeping only: copies still queued land in slots that are now
+    // empty, and any later copy into a slot is ordered after them on the copy
+    // stream and after the slot's last reader.
+    g.pool.policy.reset(g.pool.slots);
+    g.pool.policy.opt = g.stream_opt;
+    return HFMOE_OK;
+}
+
+}  // extern "C"

@@ -142,6 +142,44 @@ int hfmoe_fill_normal_bf16(uint16_t* dst_dev, uint64_t n, uint64_t seed, uint64_
 int hfmoe_fill_normal_f32(float* dst_dev, uint64_t n, uint64_t seed, uint64_t tensor,
                           uint64_t first, float mean, float std);
 
+/* ---- streamed experts: HBM expert cache and next-layer copy-ahead ----
+ * Layers registered with HFMOE_EXPERTS_HOST_PINNED copy their selected
+ * experts into an LRU pool of HBM slots (ExpertGpuCache, cuda_backend.cpp:
+ * 196-363; size from vram_budget_bytes).  Once a layer has routed, the experts
+ * predicted for the next layer -- the previous token's selection there -- are
+ * copied ahead while the layer computes (Scheduler::onLayerRouterDone /
+ * predictNextLayerExperts, src/engine/scheduler.cpp:180-219,238-388), unless
+ * that layer's winner-overlap EMA is below overlap_floor. */
+typedef struct hfmoe_stream_options {
+    int32_t prefetch_next_layer;  /* 1 (default): copy predicted next-layer experts ahead */
+    int32_t ema_predictor;        /* setPopularityPredictor(alpha, enable)
+                                     (scheduler.cpp:158-165); default 0 */
+    float ema_alpha;              /* heat blend, (0, 1]; default 0.1 */
+    float overlap_floor;          /* kSpecOverlapFloor (scheduler.cpp:51), default 0.5 */
+    float overlap_alpha;          /* kSpecOverlapAlpha (scheduler.cpp:52), default 0.5 */
+    int32_t reserved[3];
+} hfmoe_stream_options;
+
+/* InferenceStats routedPredStaged / routedPredConsumed / prefetchWasted
+ * (src/engine/inference_stats.h:25-35) and the cache's hit counts. */
+typedef struct hfmoe_stream_counters {
+    uint64_t lookups;        /* selected experts looked up */
+    uint64_t hits;           /* ... resident or already being copied ahead */
+    uint64_t misses;         /* ... copied on demand */
+    uint64_t pred_staged;    /* predicted experts copied ahead */
+    uint64_t pred_consumed;  /* copied-ahead experts a lookup then used */
+    uint64_t pred_wasted;    /* copied-ahead experts evicted unused */
+    uint64_t pred_resident;  /* predictions already resident (no copy) */
+    uint64_t copies;         /* expert weight sets copied host -> HBM */
+    int32_t slots;           /* HBM slots in the pool (0 before the first streamed call) */
+    int32_t reserved;
+} hfmoe_stream_counters;
+
+int hfmoe_stream_set_options(const hfmoe_stream_options* opt);
+int hfmoe_stream_get_options(hfmoe_stream_options* opt);
+int hfmoe_stream_read_counters(hfmoe_stream_counters* out);
+int hfmoe_stream_reset(void);  /* empty the pool, forget routing history, zero counters */
+
 /* ---- telemetry (InferenceStats gpuActiveNs / pcieBytes,
  *      src/engine/inference_stats.h:86-93) ---- */
 typedef struct hfmoe_kernel_stat {

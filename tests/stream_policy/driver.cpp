@@ -1,0 +1,70 @@
+// Replays streamed-layer calls through the library's host policy
+// (hummingflight_amd/csrc/expert_stream_policy.h) without a GPU, so the CPU
+// tests can compare every decision with the oracle's restatement.
+//
+// stdin, one command per line:
+//   reset SLOTS
+//   opt PREFETCH EMA EMA_ALPHA OVERLAP_FLOOR OVERLAP_ALPHA
+//   call LAYER NEXT_STREAMED K E1 .. EK
+// stdout per call: "L s0 c0 s1 c1 ..." (slot, copy flag per selected expert),
+// then "S e0 s0 e1 s1 ..." (copied-ahead expert and slot); at the end the
+// counters in the order of hfmoe_stream_counters.
+#include <cstdio>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "expert_stream_policy.h"
+
+int main() {
+    hf::ExpertStreamPolicy p;
+    p.reset(16);
+    std::string line;
+    while (std::getline(std::cin, line)) {
+        std::istringstream in(line);
+        std::string cmd;
+        in >> cmd;
+        if (cmd == "reset") {
+            int slots = 0;
+            in >> slots;
+            const hf::StreamPolicyOptions keep = p.opt;
+            p.reset(slots);
+            p.opt = keep;
+        } else if (cmd == "opt") {
+            int pf = 0, ema = 0;
+            in >> pf >> ema >> p.opt.ema_alpha >> p.opt.overlap_floor >> p.opt.overlap_alpha;
+            p.opt.prefetch = pf != 0;
+            p.opt.ema_predictor = ema != 0;
+        } else if (cmd == "call") {
+            int layer = 0, next = 0, k = 0;
+            in >> layer >> next >> k;
+            std::vector<int> topk(k);
+            for (int& e : topk) in >> e;
+            // The same sequence as streamed_forward_t1 (streamed.hip).
+            int held[16];
+            std::printf("L");
+            for (int r = 0; r < k; ++r) {
+                bool copy = false;
+                held[r] = p.lookup(layer, topk[r], held, r, &copy);
+                std::printf(" %d %d", held[r], copy ? 1 : 0);
+            }
+            std::printf("\nS");
+            int nheld = k;
+            for (int e : p.route_done(layer, topk.data(), k, next != 0)) {
+                if (e < 0 || nheld >= 16) continue;
+                const int s = p.stage(layer + 1, e, held, nheld);
+                if (s < 0) continue;
+                held[nheld++] = s;
+                std::printf(" %d %d", e, s);
+            }
+            std::printf("\n");
+        }
+    }
+    const hf::StreamPolicyCounters& n = p.n;
+    std::printf("C %llu %llu %llu %llu %llu %llu %llu %llu\n", (unsigned long long)n.lookups,
+                (unsigned long long)n.hits, (unsigned long long)n.misses, (unsigned long long)n.pred_staged,
+                (unsigned long long)n.pred_consumed, (unsigned long long)n.pred_wasted,
+                (unsigned long long)n.pred_resident, (unsigned long long)n.copies);
+    return 0;
+}

@@ -1,0 +1,166 @@
+"""Streamed-expert cache and copy-ahead policy, on the CPU.
+
+The oracle's restatement (oracle/stream_policy.py) is pinned first: its cache
+against a brute-force LRU over last-use times, its predictor against routing
+histories worked out by hand (gate timing at the floor, carry-over of the
+current layer's selection, a disjoint alternation that never opens the gate,
+the popularity boost changing a victim).  The library's own policy code
+(hummingflight_amd/csrc/expert_stream_policy.h), built with g++ into
+tests/stream_policy/driver, must then make the same decision at every step of
+randomised correlated routing histories.
+"""
+import os
+import random
+import shutil
+import subprocess
+
+import pytest
+
+from oracle.stream_policy import COUNTERS, Options, StreamPolicy
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DRIVER_DIR = os.path.join(HERE, "stream_policy")
+DRIVER = os.path.join(DRIVER_DIR, "driver")
+
+
+def brute_lru(slots, calls):
+    """Slots by last-use time: an empty slot (lowest index), else the oldest unheld."""
+    key, last, clock, out = [None] * slots, [0] * slots, 0, []
+    for layer, topk in calls:
+        held, res = [], []
+        for e in topk:
+            k = (layer, e)
+            if k in key:
+                s, copy = key.index(k), False
+            else:
+                empty = [i for i in range(slots) if key[i] is None and i not in held]
+                s = empty[0] if empty else min((i for i in range(slots) if i not in held), key=lambda i: last[i])
+                key[s], copy = k, True
+            clock += 1
+            last[s] = clock
+            held.append(s)
+            res.append((s, copy))
+        out.append(res)
+    return out
+
+
+def test_oracle_cache_is_lru():
+    rng = random.Random(5)
+    for case in range(200):
+        k = rng.randint(1, 4)
+        slots = rng.randint(k, 3 * k + 2)
+        calls = [(rng.randrange(3), rng.sample(range(12), k)) for _ in range(40)]
+        p = StreamPolicy(slots, Options(prefetch=False))
+        got = [p.call(layer, topk, True)[0] for layer, topk in calls]
+        assert got == brute_lru(slots, calls), case
+        assert p.n["hits"] + p.n["misses"] == p.n["lookups"] == 40 * k
+        assert p.n["copies"] == p.n["misses"]
+
+
+def run_tokens(p, layers, tokens):
+    """tokens: list of per-layer selections; layer l+1 is streamed for l < layers-1."""
+    for sel in tokens:
+        for layer in range(layers):
+            p.call(layer, sel[layer], layer + 1 < layers)
+
+
+def test_oracle_gate_opens_at_floor():
+    # Same routing every token.  A layer's overlap EMA is 0 after its first
+    # event and 0.5 after its second, so layer 1's guesses pass a 0.5 floor
+    # from the third token on (already resident: no copy).
+    sel = [[3, 4], [5, 6]]
+    p = StreamPolicy(16)
+    run_tokens(p, 2, [sel] * 4)
+    assert (p.n["misses"], p.n["hits"], p.n["pred_resident"], p.n["pred_staged"]) == (4, 12, 4, 0)
+    # A floor just above 0.5 waits for the third event (EMA 0.75).
+    p = StreamPolicy(16, Options(overlap_floor=0.51))
+    run_tokens(p, 2, [sel] * 4)
+    assert p.n["pred_resident"] == 2
+
+
+def test_oracle_disjoint_alternation_never_stages():
+    a, b = [[0, 1], [2, 3]], [[4, 5], [6, 7]]
+    p = StreamPolicy(4)  # too small to keep both: every token misses
+    run_tokens(p, 2, [a, b] * 5)
+    assert p.n["pred_staged"] == p.n["pred_resident"] == 0
+    assert p.n["misses"] == 40  # 10 tokens x 4 keys, none kept from the token before
+
+
+def test_oracle_carry_over_consumed_and_wasted():
+    # Floor 0: on the first token layer 1 has no history, so layer 0's own
+    # selection is copied ahead as layer 1's guess.  Expert 3 is then used
+    # (consumed), expert 4 never is; evicting it later counts as wasted.
+    p = StreamPolicy(4, Options(overlap_floor=0.0))
+    looked, staged = p.call(0, [3, 4], True)
+    assert looked == [(0, True), (1, True)] and staged == [(3, 2), (4, 3)]
+    looked, staged = p.call(1, [3, 5], False)
+    assert looked == [(2, False), (0, True)]
+    assert (p.n["pred_staged"], p.n["pred_consumed"], p.n["pred_wasted"]) == (2, 1, 0)
+    p.call(1, [6, 7], False)  # least recent unheld: slot 1 (expert 0:4), then slot 3 (1:4, unused)
+    assert (p.n["pred_wasted"], p.find((1, 4)), p.find((0, 4))) == (1, -1, -1)
+
+
+def test_oracle_popularity_boost_changes_victims():
+    calls = [(0, [0, 1]), (0, [2, 3]), (0, [4, 5])]
+    plain = StreamPolicy(4, Options(prefetch=False))
+    boosted = StreamPolicy(4, Options(prefetch=False, ema_predictor=True))
+    for layer, topk in calls:
+        a = plain.call(layer, topk, False)[0]
+        b = boosted.call(layer, topk, False)[0]
+    # Plain LRU evicts experts 0 and 1.  Boosted: 0 (first routed, hottest on a
+    # tie) and 2 are protected for one sweep, so 1 and 3 go instead.
+    assert a == [(0, True), (1, True)]
+    assert b == [(1, True), (3, True)]
+
+
+def correlated_history(rng, layers, tokens, k, n_experts, p_change):
+    cur = [rng.sample(range(n_experts), k) for _ in range(layers)]
+    hist = []
+    for _ in range(tokens):
+        step = []
+        for layer in range(layers):
+            sel = list(cur[layer])
+            for i in range(k):
+                if rng.random() < p_change:
+                    sel[i] = rng.choice([e for e in range(n_experts) if e not in sel])
+            cur[layer] = sel
+            step.append(sel)
+        hist.append(step)
+    return hist
+
+
+@pytest.fixture(scope="module")
+def driver():
+    if not shutil.which("g++"):
+        pytest.skip("g++ not available")
+    subprocess.run(["make", "-s", "-C", DRIVER_DIR], check=True)
+    return DRIVER
+
+
+def test_library_policy_matches_oracle(driver):
+    rng = random.Random(11)
+    for case in range(60):
+        k = rng.choice([1, 2, 4, 8])
+        layers = rng.randint(1, 4)
+        slots = rng.choice([2 * k, 3 * k, layers * k, 2 * layers * k + 1])
+        opt = Options(prefetch=rng.random() < 0.8, ema_predictor=rng.random() < 0.5,
+                      ema_alpha=rng.choice([0.1, 0.5, 1.0]), overlap_floor=rng.choice([0.0, 0.3, 0.5, 0.8]),
+                      overlap_alpha=rng.choice([0.5, 0.3, 1.0]))
+        hist = correlated_history(rng, layers, 12, k, 24, rng.choice([0.0, 0.2, 0.5, 1.0]))
+        lines = [f"opt {int(opt.prefetch)} {int(opt.ema_predictor)} {opt.ema_alpha} {opt.overlap_floor} "
+                 f"{opt.overlap_alpha}", f"reset {slots}"]
+        p = StreamPolicy(slots, opt)
+        want = []
+        for step in hist:
+            for layer in range(layers):
+                sel = step[layer]
+                lines.append(f"call {layer} {int(layer + 1 < layers)} {k} " + " ".join(map(str, sel)))
+                looked, staged = p.call(layer, sel, layer + 1 < layers)
+                want.append("L" + "".join(f" {s} {int(c)}" for s, c in looked))
+                want.append("S" + "".join(f" {e} {s}" for e, s in staged))
+        want.append("C " + " ".join(str(p.n[c]) for c in COUNTERS))
+        r = subprocess.run([driver], input="\n".join(lines) + "\n", capture_output=True, text=True, check=True)
+        got = r.stdout.strip().split("\n")
+        assert len(got) == len(want), case
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert g.strip() == w.strip(), f"case {case} line {i}: library {g!r} oracle {w!r}"
