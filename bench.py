@@ -276,16 +276,41 @@ def run_grouped(args, workload: str) -> dict:
     return res
 
 
-def run_streamed(args) -> dict:
-    """8 chained layers, routed experts in pinned host RAM, T=1 per step."""
+def stream_counters() -> dict:
+    c = capi.StreamCounters()
+    capi.call("hfmoe_stream_read_counters", C.byref(c))
+    return c.as_dict()
+
+
+def run_streamed(args, cached: bool = False) -> dict:
+    """8 chained layers, routed experts in pinned host RAM, T=1 per step.
+
+    cached: an HBM expert cache of --cache-gb and a run of correlated tokens
+    (each token's input = a shared base + --token-noise x N(0, 1)), so that
+    consecutive tokens reuse experts and the next-layer copy-ahead has history
+    to predict from.  Otherwise the pool holds two layers' selections and the
+    tokens are independent: every selected expert crosses PCIe."""
     shape = synth.LayerShape(**FULL)
     n_layers = 8
-    capi.call("hfmoe_configure", shape.config(max_tokens=1))
+    cfg = shape.config(max_tokens=1)
+    if cached:
+        cfg.vram_budget_bytes = int(args.cache_gb * 2**30)
+    capi.call("hfmoe_configure", cfg)
+    opt = capi.StreamOptions()
+    capi.call("hfmoe_stream_get_options", C.byref(opt))
+    opt.overlap_floor = args.overlap_floor
+    capi.call("hfmoe_stream_set_options", C.byref(opt))
     layers = [synth.DeviceLayer(shape, layer=l, seed=args.seed, experts_on_host=True, with_norm=True,
                                 distinct_experts=args.distinct_experts) for l in range(n_layers)]
     d = shape.hidden
     ntok = args.warmup + 2 * args.steps
-    h = synth.make_x_dev(ntok, d, seed=args.seed)
+    if cached:
+        rng = np.random.default_rng(args.seed)
+        base = rng.standard_normal(d).astype(np.float32)
+        xs = base + args.token_noise * rng.standard_normal((ntok, d)).astype(np.float32)
+        h = capi.DeviceBuffer.of(xs.astype(np.float32))
+    else:
+        h = synth.make_x_dev(ntok, d, seed=args.seed)
     blk = capi.load().hfmoe_mlp_block
     cursor = [0]
 
@@ -302,9 +327,14 @@ def run_streamed(args) -> dict:
     capi.call("hfmoe_synchronize")
     p0, a0 = C.c_uint64(), C.c_uint64()
     capi.call("hfmoe_stats", C.byref(p0), C.byref(a0))
+    n0 = stream_counters()
     sec = time_steps(step, args.steps, 0)
     p1, a1 = C.c_uint64(), C.c_uint64()
     capi.call("hfmoe_stats", C.byref(p1), C.byref(a1))
+    n1 = stream_counters()
+    cache = {c: n1[c] - n0[c] for c in n1 if c != "slots"}
+    cache["slots"] = n1["slots"]
+    cache["hit_rate"] = round(cache["hits"] / max(cache["lookups"], 1), 4)
     prof, sec_prof = profiled_pass(step, args.steps)
     pcie = (p1.value - p0.value) / args.steps
     # Pinned host -> HBM copy rate of one layer's 8 selected experts, for the bound.
@@ -320,17 +350,23 @@ def run_streamed(args) -> dict:
     res = {
         "value": 1.0 / sec,
         "ms_per_step": sec * 1e3,
-        "config": {"workload": "moe_streamed_chain", "tokens": 1, "layers": n_layers, "hidden": d,
+        "config": {"workload": "moe_streamed_chain_cached" if cached else "moe_streamed_chain", "tokens": 1,
+                   "layers": n_layers, "hidden": d,
                    "moe_intermediate": shape.inter, "routed_experts": shape.n_experts,
                    "shared_experts": shape.n_shared, "top_k": shape.top_k, "n_group": shape.n_group,
                    "topk_group": shape.topk_group,
                    "weights": f"routed experts in pinned host RAM ({args.distinct_experts} distinct weight "
                               f"sets per layer, every expert its own cache key); routers, shared experts "
-                              f"and norms in HBM"},
+                              f"and norms in HBM",
+                   "hbm_expert_cache_gb": args.cache_gb if cached else None,
+                   "copy_ahead_overlap_floor": args.overlap_floor,
+                   "tokens_input": (f"correlated: base + {args.token_noise} x N(0,1) per token" if cached
+                                    else "independent N(0,1) tokens")},
         "roofline": {"bound": "pcie", "kernel": "hipMemcpyAsync host->device", "achieved": round(achieved, 1),
                      "peak": round(h2d_gbs, 1), "unit": "GB/s", "frac": round(achieved / h2d_gbs, 4),
                      "traffic": int(pcie), "peak_source": "measured pinned copy of 8 experts"},
         "pcie_bytes_per_token": int(pcie),
+        "expert_cache": cache,
         "ms_per_step_with_kernel_events": sec_prof * 1e3,
         "kernels": kernel_table(prof, {}),
     }
@@ -383,6 +419,8 @@ METRICS = {
     "batched": "MoE-layer batched-decode tokens/s + HBM GB/s at d=6144, 256e top-8, T=64 Zipf(1.1)",
     "prefill": "MoE-layer prefill tokens/s + BF16 MFMA TFLOP/s at d=6144, 256e top-8, T=4096",
     "streamed": "8-layer streamed-expert decode tokens/s + PCIe GB/s at d=6144, 256e top-8",
+    "streamed_cached": "8-layer streamed-expert decode tokens/s with an HBM expert cache and next-layer "
+                       "copy-ahead, correlated tokens, at d=6144, 256e top-8",
 }
 
 
@@ -391,10 +429,17 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "batched", "prefill", "streamed", "copy"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
+    ap.add_argument("--cache-gb", type=float, default=40.0,
+                    help="streamed_cached: HBM expert cache size (a quarter of the 8 layers' routed experts)")
+    ap.add_argument("--token-noise", type=float, default=0.35,
+                    help="streamed_cached: per-token deviation from the shared base input")
+    ap.add_argument("--overlap-floor", type=float, default=0.5,
+                    help="streamed: winner-overlap EMA below which next-layer copy-ahead is skipped")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -402,7 +447,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
-    defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3), "copy": (5, 0)}
+    defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
+                "streamed_cached": (30, 10), "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
     args.warmup = d_warm if args.warmup is None else args.warmup
@@ -413,8 +459,8 @@ def main() -> int:
         return 0
     if args.workload == "decode":
         res = run_decode(args)
-    elif args.workload == "streamed":
-        res = run_streamed(args)
+    elif args.workload in ("streamed", "streamed_cached"):
+        res = run_streamed(args, cached=args.workload == "streamed_cached")
     else:
         res = run_grouped(args, args.workload)
     line = {"metric": METRICS[args.workload], "value": round(res.pop("value"), 2), "unit": "tokens/s",
