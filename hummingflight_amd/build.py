@@ -1,6 +1,7 @@
 """Build libhfmoe.so (HIP, gfx950) in-tree with hipcc.
 
-Every .hip file under csrc/ is compiled for gfx950 only and linked into
+Every .hip file (device and host code) and .cpp file (host code) under csrc/
+is compiled with hipcc for gfx950 only and linked into
 hummingflight_amd/libhfmoe.so.  Packed FP32 instruction generation is disabled
 (-Xclang -target-feature -Xclang -packed-fp32-ops) for all device code.
 """
@@ -40,7 +41,7 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     """Compile every HIP source and link the shared library; returns its path."""
     os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"

@@ -69,6 +69,21 @@ class StreamCounters(C.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
 
 
+class SafetensorsStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("total", "accepted", "rejected", "duplicate_rejected", "dtype_rejected",
+                                          "f32_allowed_accepted", "shape_rejected", "bounds_rejected",
+                                          "byte_mismatch_rejected", "alignment_rejected")] + \
+               [("shards", C.c_int32), ("reserved", C.c_int32)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}
+
+
+class TensorInfo(C.Structure):
+    _fields_ = [("dtype", C.c_char * 8), ("ndim", C.c_int32), ("reserved", C.c_int32),
+                ("shape", C.c_int64 * 8), ("nbytes", C.c_uint64), ("file_offset", C.c_uint64)]
+
+
 # (name, restype, argtypes) for every entry point of include/hfmoe.h.
 _SIGS = [
     ("hfmoe_init", C.c_int, [C.c_int]),
@@ -110,6 +125,11 @@ _SIGS = [
     ("hfmoe_stream_get_options", C.c_int, [C.POINTER(StreamOptions)]),
     ("hfmoe_stream_read_counters", C.c_int, [C.POINTER(StreamCounters)]),
     ("hfmoe_stream_reset", C.c_int, []),
+    ("hfmoe_checkpoint_open", C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    ("hfmoe_checkpoint_stats", C.c_int, [C.c_void_p, C.POINTER(SafetensorsStats)]),
+    ("hfmoe_checkpoint_tensor", C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(TensorInfo)]),
+    ("hfmoe_checkpoint_load_moe_layer", C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    ("hfmoe_checkpoint_close", None, [C.c_void_p]),
     ("hfmoe_stats", C.c_int, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
 ]
 

@@ -180,6 +180,47 @@ int hfmoe_stream_get_options(hfmoe_stream_options* opt);
 int hfmoe_stream_read_counters(hfmoe_stream_counters* out);
 int hfmoe_stream_reset(void);  /* empty the pool, forget routing history, zero counters */
 
+/* ---- checkpoints: safetensors shards -> registered MoE layers ----
+ * WeightIndex::build (src/model/weight_index.cpp:84-266) over strict shard
+ * parsing (SafeTensorsFile::open with strictStOpts, safetensors.cpp:60-240,
+ * weight_index.cpp:20-27): BF16 only, F32 allowed for
+ * "e_score_correction_bias"; rejected tensors are counted and skipped. */
+typedef struct hfmoe_checkpoint hfmoe_checkpoint;  /* opaque */
+
+typedef struct hfmoe_safetensors_stats {  /* SafeTensorsStats (safetensors.h:50-61) */
+    uint64_t total, accepted, rejected;
+    uint64_t duplicate_rejected, dtype_rejected, f32_allowed_accepted;
+    uint64_t shape_rejected, bounds_rejected, byte_mismatch_rejected, alignment_rejected;
+    int32_t shards;
+    int32_t reserved;
+} hfmoe_safetensors_stats;
+
+typedef struct hfmoe_tensor_info {  /* TensorInfo / TensorLocation (weight_index.h:14-26) */
+    char dtype[8];
+    int32_t ndim;
+    int32_t reserved;
+    int64_t shape[8];
+    uint64_t nbytes;
+    uint64_t file_offset;  /* absolute byte offset of the data in its shard */
+} hfmoe_tensor_info;
+
+/* path: a directory of *.safetensors shards (with model.safetensors.index.json
+ * when present: its weight_map picks each tensor's shard), or one shard file.
+ * Parsing needs no device.  Fails on an unreadable shard, a header length that
+ * is not a multiple of 8 or a header that is not a JSON object. */
+int hfmoe_checkpoint_open(const char* path, hfmoe_checkpoint** out);
+int hfmoe_checkpoint_stats(const hfmoe_checkpoint* ck, hfmoe_safetensors_stats* out);
+int hfmoe_checkpoint_tensor(const hfmoe_checkpoint* ck, const char* name, hfmoe_tensor_info* out);
+/* Copies model.layers.<layer>.mlp.{gate.weight, gate.e_score_correction_bias,
+ * shared_experts.*, experts.<e>.{gate,up,down}_proj.weight} and
+ * post_attention_layernorm.weight (shapes checked against hfmoe_configure) to
+ * HBM -- routed experts to HBM or pinned host RAM per experts_location, each
+ * expert as [gate | up | down] (scheduler.cpp:437-471) -- and registers the
+ * layer.  The checkpoint owns these copies. */
+int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts_location);
+/* Unregisters the layers loaded from ck, frees their copies and the index. */
+void hfmoe_checkpoint_close(hfmoe_checkpoint* ck);
+
 /* ---- telemetry (InferenceStats gpuActiveNs / pcieBytes,
  *      src/engine/inference_stats.h:86-93) ---- */
 typedef struct hfmoe_kernel_stat {
