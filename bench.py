@@ -384,6 +384,82 @@ def run_streamed(args, cached: bool = False) -> dict:
     return res
 
 
+def run_load(args) -> None:
+    """Checkpoint loading: one MoE layer (full d=6144 / I=2048 shapes, --load-experts
+    routed experts) written as a safetensors shard, then timed through
+    hfmoe_checkpoint_open + hfmoe_checkpoint_load_moe_layer into HBM.  The shard
+    was just written, so it is read from the page cache: the bound is the
+    host-memory read and the host->device copy, not the disk."""
+    import shutil
+    import tempfile
+    shape = synth.LayerShape(**dict(FULL, n_experts=args.load_experts))
+    capi.call("hfmoe_configure", shape.config(max_tokens=1))
+    d, I, E = shape.hidden, shape.inter, shape.n_experts
+    p = "model.layers.0.mlp."
+    tensors = [(p + "gate.weight", "BF16", [E, d]), (p + "gate.e_score_correction_bias", "F32", [E]),
+               (p + "shared_experts.gate_proj.weight", "BF16", [I, d]),
+               (p + "shared_experts.up_proj.weight", "BF16", [I, d]),
+               (p + "shared_experts.down_proj.weight", "BF16", [d, I])]
+    for e in range(E):
+        tensors += [(p + f"experts.{e}.gate_proj.weight", "BF16", [I, d]),
+                    (p + f"experts.{e}.up_proj.weight", "BF16", [I, d]),
+                    (p + f"experts.{e}.down_proj.weight", "BF16", [d, I])]
+    header, off = {}, 0
+    for name, dt, shp in tensors:
+        nb = int(np.prod(shp)) * (2 if dt == "BF16" else 4)
+        header[name] = {"dtype": dt, "shape": shp, "data_offsets": [off, off + nb]}
+        off += nb + (-nb) % 8
+    h = json.dumps(header).encode()
+    h += b" " * ((-len(h)) % 8)
+    tmp = tempfile.mkdtemp(prefix="hfmoe_ckpt_")
+    path = os.path.join(tmp, "model-00001-of-00001.safetensors")
+    buf = capi.DeviceBuffer(2 * I * d)
+    t0 = time.perf_counter()
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little"))
+        f.write(h)
+        for i, (name, dt, shp) in enumerate(tensors):
+            n = int(np.prod(shp))
+            if dt == "BF16":
+                synth.fill_bf16(buf.ptr, n, args.seed, i, 0.0, 0.02)
+                a = buf.download(np.uint16, n)
+            else:
+                a = np.zeros(n, np.float32)
+            f.write(a.tobytes())
+            f.write(bytes((-a.nbytes) % 8))
+    t_write = time.perf_counter() - t0
+    buf.free()
+    total = sum(int(np.prod(shp)) * (2 if dt == "BF16" else 4) for _, dt, shp in tensors)
+    L = capi.load()
+    ck = C.c_void_p()
+    t0 = time.perf_counter()
+    capi.call("hfmoe_checkpoint_open", path.encode(), C.byref(ck))
+    t_open = time.perf_counter() - t0
+    capi.call("hfmoe_checkpoint_load_moe_layer", ck, 0, capi.EXPERTS_DEVICE)
+    capi.call("hfmoe_synchronize")
+    t_load = time.perf_counter() - t0
+    L.hfmoe_checkpoint_close(ck)
+    shutil.rmtree(tmp, ignore_errors=True)
+    # The bound: a pinned host -> HBM copy of the same size class.
+    nbytes = 1 << 30
+    src = capi.PinnedBuffer(nbytes)
+    dst = capi.DeviceBuffer(nbytes)
+    capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    h2d = 3 * nbytes / (time.perf_counter() - t0) / 1e9
+    src.free()
+    dst.free()
+    print(json.dumps({"metric": "MoE layer checkpoint load GB/s (safetensors shard in page cache -> HBM)",
+                      "value": round(total / t_load / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+                      "higher_is_better": True, "bytes": total, "seconds": round(t_load, 3),
+                      "open_seconds": round(t_open, 4), "write_seconds": round(t_write, 2),
+                      "pinned_h2d_gbs": round(h2d, 1), "frac_of_pinned_h2d": round(total / t_load / 1e9 / h2d, 3),
+                      "config": {"workload": "checkpoint_load", "hidden": d, "moe_intermediate": I,
+                                 "routed_experts": E, "shared_experts": 1}}), flush=True)
+
+
 def run_copy(args) -> None:
     """Counter calibration: 4 GiB device-to-device copies (HIP's own copy kernel)."""
     n = 4 << 30
@@ -430,7 +506,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "copy"])
+                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "load", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
@@ -440,6 +516,8 @@ def main() -> int:
                     help="streamed_cached: per-token deviation from the shared base input")
     ap.add_argument("--overlap-floor", type=float, default=0.5,
                     help="streamed: winner-overlap EMA below which next-layer copy-ahead is skipped")
+    ap.add_argument("--load-experts", type=int, default=64,
+                    help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
@@ -448,13 +526,13 @@ def main() -> int:
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
     defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
-                "streamed_cached": (30, 10), "copy": (5, 0)}
+                "streamed_cached": (30, 10), "load": (1, 0), "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
     args.warmup = d_warm if args.warmup is None else args.warmup
     capi.call("hfmoe_init", 0)
-    if args.workload == "copy":
-        run_copy(args)
+    if args.workload in ("copy", "load"):
+        (run_copy if args.workload == "copy" else run_load)(args)
         capi.load().hfmoe_shutdown()
         return 0
     if args.workload == "decode":

@@ -29,6 +29,7 @@
 #include <dirent.h>
 #include <memory>
 #include <set>
+#include <thread>
 
 #include "hf_api_internal.h"
 
@@ -378,6 +379,74 @@ bool read_index(const std::string& path, std::map<std::string, std::string>& map
     return true;
 }
 
+// Copies of one layer load.  Host-to-HBM copies go through a ring of pinned
+// staging buffers: the host threads fill slot i (memcpy out of the mapped
+// shard) while the copy stream moves slot i-1 to HBM; a slot is refilled
+// only after its previous transfer finished.  Host-to-pinned copies are plain
+// threaded memcpy.  The mapped pages are never handed to the runtime.
+struct CopyJob {
+    const uint8_t* src;
+    void* dst;
+    size_t bytes;
+    bool to_device;
+};
+
+void parallel_memcpy(uint8_t* dst, const uint8_t* src, size_t bytes, int threads) {
+    const size_t min_part = 4u << 20;
+    const int n = (int)std::max<size_t>(1, std::min<size_t>((size_t)threads, bytes / min_part));
+    if (n == 1) {
+        memcpy(dst, src, bytes);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const size_t part = (bytes + n - 1) / n;
+    for (int i = 0; i < n; ++i) {
+        const size_t b = (size_t)i * part, e = std::min(bytes, b + part);
+        if (b < e) pool.emplace_back([=] { memcpy(dst + b, src + b, e - b); });
+    }
+    for (auto& t : pool) t.join();
+}
+
+hipError_t run_copies(const std::vector<CopyJob>& jobs) {
+    const int threads = (int)std::min(16u, std::max(1u, std::thread::hardware_concurrency()));
+    constexpr int kSlots = 4;
+    constexpr size_t kSlotBytes = 32u << 20;
+    uint8_t* stage[kSlots] = {};
+    hipEvent_t done[kSlots] = {};
+    bool busy[kSlots] = {};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < kSlots && e == hipSuccess; ++i) {
+        e = hipHostMalloc(reinterpret_cast<void**>(&stage[i]), kSlotBytes, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
+    }
+    int slot = 0;
+    for (const CopyJob& j : jobs) {
+        if (e != hipSuccess) break;
+        if (!j.to_device) {
+            parallel_memcpy(static_cast<uint8_t*>(j.dst), j.src, j.bytes, threads);
+            continue;
+        }
+        for (size_t off = 0; off < j.bytes && e == hipSuccess; off += kSlotBytes) {
+            const size_t n = std::min(kSlotBytes, j.bytes - off);
+            if (busy[slot]) e = hipEventSynchronize(done[slot]);
+            if (e != hipSuccess) break;
+            parallel_memcpy(stage[slot], j.src + off, n, threads);
+            e = hipMemcpyAsync(static_cast<uint8_t*>(j.dst) + off, stage[slot], n, hipMemcpyHostToDevice,
+                               g.copy_stream);
+            if (e == hipSuccess) e = hipEventRecord(done[slot], g.copy_stream);
+            busy[slot] = true;
+            slot = (slot + 1) % kSlots;
+        }
+    }
+    const hipError_t s = hipStreamSynchronize(g.copy_stream);
+    if (e == hipSuccess) e = s;
+    for (int i = 0; i < kSlots; ++i) {
+        if (done[i]) hipEventDestroy(done[i]);
+        if (stage[i]) hipHostFree(stage[i]);
+    }
+    return e;
+}
+
 const TensorRef* find2(const hfmoe_checkpoint& ck, const std::string& name, int64_t r, int64_t c,
                        const char* dtype, std::string& err) {
     auto it = ck.tensors.find(name);
@@ -508,11 +577,13 @@ int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts
         for (void* p : L.dev) hipFree(p);
         for (void* p : L.host) hipHostFree(p);
     };
+    std::vector<CopyJob> jobs;
     auto to_dev = [&](const void* src, size_t bytes, void** dst) -> hipError_t {
         hipError_t e = hipMalloc(dst, bytes);
         if (e != hipSuccess) return e;
         L.dev.push_back(*dst);
-        return hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+        jobs.push_back({static_cast<const uint8_t*>(src), *dst, bytes, true});
+        return hipSuccess;
     };
     hipError_t e = hipSuccess;
     void *router_d = nullptr, *bias_d = nullptr, *sg_d = nullptr, *su_d = nullptr, *sd_d = nullptr, *norm_d = nullptr;
@@ -538,8 +609,9 @@ int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts
     // Routed experts: one block, expert e at e * 3*I*d elements as [gate | up | down].
     const size_t proj = (size_t)I * d, eb = 3 * proj * 2;
     uint16_t* block = nullptr;
+    const bool on_dev = experts_location == HFMOE_EXPERTS_DEVICE;
     if (e == hipSuccess) {
-        if (experts_location == HFMOE_EXPERTS_DEVICE) {
+        if (on_dev) {
             e = hipMalloc(reinterpret_cast<void**>(&block), eb * E);
             if (e == hipSuccess) L.dev.push_back(block);
         } else {
@@ -549,14 +621,12 @@ int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts
     }
     std::vector<const uint16_t*> table(3 * E);
     for (int64_t ei = 0; ei < E && e == hipSuccess; ++ei)
-        for (int q = 0; q < 3 && e == hipSuccess; ++q) {
+        for (int q = 0; q < 3; ++q) {
             uint16_t* dst = block + ei * 3 * proj + q * proj;
             table[3 * ei + q] = dst;
-            if (experts_location == HFMOE_EXPERTS_DEVICE)
-                e = hipMemcpy(dst, ex[3 * ei + q]->data(), proj * 2, hipMemcpyHostToDevice);
-            else
-                memcpy(dst, ex[3 * ei + q]->data(), proj * 2);
+            jobs.push_back({ex[3 * ei + q]->data(), dst, proj * 2, on_dev});
         }
+    if (e == hipSuccess) e = run_copies(jobs);
     if (e != hipSuccess) {
         cleanup();
         return fail_hip(e, "checkpoint layer upload");
