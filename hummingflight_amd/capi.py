@@ -44,6 +44,11 @@ class LayerWeights(C.Structure):
                 ("reserved", C.c_int32)]
 
 
+class DenseWeights(C.Structure):
+    _fields_ = [("gate_dev", C.c_void_p), ("up_dev", C.c_void_p), ("down_dev", C.c_void_p),
+                ("post_attention_norm_dev", C.c_void_p), ("intermediate", C.c_int32), ("reserved", C.c_int32)]
+
+
 class RouteDebug(C.Structure):
     _fields_ = [("logits_dev", C.c_void_p), ("idx_dev", C.c_void_p), ("weight_dev", C.c_void_p),
                 ("offsets_dev", C.c_void_p), ("perm_dev", C.c_void_p)]
@@ -99,6 +104,8 @@ _SIGS = [
      [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(RouteDebug)]),
     ("hfmoe_moe_layer", C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
     ("hfmoe_mlp_block", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
+    ("hfmoe_register_dense_layer", C.c_int, [C.c_int, C.POINTER(DenseWeights)]),
+    ("hfmoe_dense_mlp_forward", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_expert_cache_config", C.c_int, [C.c_int, C.c_int]),
     ("hfmoe_expert_cache_shutdown", None, []),
     ("hfmoe_experts_enabled", C.c_int, []),
@@ -129,6 +136,7 @@ _SIGS = [
     ("hfmoe_checkpoint_stats", C.c_int, [C.c_void_p, C.POINTER(SafetensorsStats)]),
     ("hfmoe_checkpoint_tensor", C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(TensorInfo)]),
     ("hfmoe_checkpoint_load_moe_layer", C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+    ("hfmoe_checkpoint_load_dense_layer", C.c_int, [C.c_void_p, C.c_int]),
     ("hfmoe_checkpoint_close", None, [C.c_void_p]),
     ("hfmoe_stats", C.c_int, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
 ]

@@ -196,6 +196,7 @@ void hfmoe_shutdown(void) {
     g.layers.clear();
     free_workspace();
     grouped_workspace_free();
+    dense_workspace_free();
     prof_drain();
     for (auto ev : g.event_pool) hipEventDestroy(ev);
     g.event_pool.clear();
@@ -260,6 +261,7 @@ int hfmoe_configure(const hfmoe_config* cfg) {
         if (kv.second.etab_dev) hipFree(kv.second.etab_dev);
     g.layers.clear();
     stream_pool_release();
+    dense_workspace_free();
     rc = alloc_workspace();
     if (rc) return rc;
     rc = grouped_workspace_alloc();
@@ -331,6 +333,7 @@ int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out
         return fail(HFMOE_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
     hipStream_t s = pick_stream(stream);
     LayerState& L = it->second;
+    if (L.dense) return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d is a dense MLP layer", layer);
     if (L.location == HFMOE_EXPERTS_HOST_PINNED) {
         if (T != 1) return fail(HFMOE_ERR_UNSUPPORTED, "streamed experts support T=1 only");
         return streamed_forward_t1(layer, L, x_dev, out_dev, s, dbg);
@@ -371,7 +374,7 @@ int hfmoe_mlp_block(int layer, float* h_dev, int32_t T, void* stream) {
     hipError_t e = launch_rmsnorm(h_dev, it->second.norm_w, xn, T, g.cfg.d, g.cfg.eps, s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "rmsnorm launch");
-    rc = hfmoe_moe_forward(layer, xn, T, mo, s);
+    rc = it->second.dense ? hfmoe_dense_mlp_forward(layer, xn, T, mo, s) : hfmoe_moe_forward(layer, xn, T, mo, s);
     if (rc) return rc;
     prof_begin(p, "residual_add", s);
     e = launch_add_inplace(h_dev, mo, (size_t)T * g.cfg.d, s);

@@ -649,6 +649,60 @@ int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts
     return HFMOE_OK;
 }
 
+int hfmoe_checkpoint_load_dense_layer(hfmoe_checkpoint* ck, int layer) {
+    int rc = require_cfg();
+    if (rc) return rc;
+    if (!ck) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null checkpoint");
+    if (ck->loaded.count(layer)) return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d already loaded", layer);
+    const int64_t d = g.cfg.d;
+    const std::string pre = "model.layers." + std::to_string(layer) + ".";
+    auto it = ck->tensors.find(pre + "mlp.gate_proj.weight");
+    if (it == ck->tensors.end())
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "tensor %smlp.gate_proj.weight is missing", pre.c_str());
+    const int64_t inter = it->second.shape.empty() ? 0 : it->second.shape[0];
+    std::string err;
+    const TensorRef* gt = find2(*ck, pre + "mlp.gate_proj.weight", inter, d, "BF16", err);
+    const TensorRef* ut = gt ? find2(*ck, pre + "mlp.up_proj.weight", inter, d, "BF16", err) : nullptr;
+    const TensorRef* dt = ut ? find2(*ck, pre + "mlp.down_proj.weight", d, inter, "BF16", err) : nullptr;
+    if (!dt) return fail(HFMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+    const TensorRef* norm = nullptr;
+    if (ck->tensors.count(pre + "post_attention_layernorm.weight")) {
+        norm = find2(*ck, pre + "post_attention_layernorm.weight", d, 0, "BF16", err);
+        if (!norm) return fail(HFMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+    }
+    LoadedLayer L;
+    std::vector<CopyJob> jobs;
+    void* p[4] = {};
+    const TensorRef* src[4] = {gt, ut, dt, norm};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 4 && e == hipSuccess; ++i) {
+        if (!src[i]) continue;
+        e = hipMalloc(&p[i], src[i]->bytes());
+        if (e == hipSuccess) {
+            L.dev.push_back(p[i]);
+            jobs.push_back({src[i]->data(), p[i], src[i]->bytes(), true});
+        }
+    }
+    if (e == hipSuccess) e = run_copies(jobs);
+    if (e != hipSuccess) {
+        for (void* q : L.dev) hipFree(q);
+        return fail_hip(e, "checkpoint dense layer upload");
+    }
+    hfmoe_dense_weights w{};
+    w.gate_dev = static_cast<const uint16_t*>(p[0]);
+    w.up_dev = static_cast<const uint16_t*>(p[1]);
+    w.down_dev = static_cast<const uint16_t*>(p[2]);
+    w.post_attention_norm_dev = static_cast<const uint16_t*>(p[3]);
+    w.intermediate = (int32_t)inter;
+    rc = hfmoe_register_dense_layer(layer, &w);
+    if (rc) {
+        for (void* q : L.dev) hipFree(q);
+        return rc;
+    }
+    ck->loaded[layer] = std::move(L);
+    return HFMOE_OK;
+}
+
 void hfmoe_checkpoint_close(hfmoe_checkpoint* ck) {
     if (!ck) return;
     for (auto& kv : ck->loaded) {

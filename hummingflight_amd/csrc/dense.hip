@@ -1,0 +1,177 @@
+// dense.hip -- the dense MLP layers (GLMForward::denseMlp, glm_forward.cpp:410-432).
+//
+// out = Wd . (silu(Wg . x) * (Wu . x)) with the dense intermediate size
+// (intermediateSize, config.h:16; 12288 at GLM-5.2 against 2048 per routed
+// expert).  No new kernels: the matrices are the same [out, in] BF16 layout as
+// an expert's, so
+//   T = 1:  the decode GEMVs multiply them as a "shared expert" of
+//           inter / slice slices (the down GEMV sums the slices' partial
+//           products in a fixed order), no routed slots;
+//   T > 1:  the grouped GEMM multiplies every token row by the one weight set
+//           (one group, no dispatch): gate/up with the SwiGLU epilogue into
+//           h (BF16 hi + lo), then down straight into out.
+#include "hf_api_internal.h"
+#include "hf_grouped.h"
+
+namespace hf {
+
+void dense_workspace_free() {
+    DenseWorkspace& w = g.dws;
+    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl})
+        if (p) hipFree(p);
+    w = DenseWorkspace{};
+}
+
+static int dense_workspace_reserve(int inter) {
+    DenseWorkspace& w = g.dws;
+    const int tokens = g.max_tokens > 1 && g.gws.xh ? g.max_tokens : 0;
+    if (inter <= w.inter && tokens <= w.tokens) return HFMOE_OK;
+    dense_workspace_free();
+    hipError_t e = hipMalloc(&w.h1, sizeof(float) * (size_t)inter);
+    if (e == hipSuccess && tokens) e = hipMalloc(&w.hh, 2 * (size_t)tokens * inter);
+    if (e == hipSuccess && tokens) e = hipMalloc(&w.hl, 2 * (size_t)tokens * inter);
+    if (e != hipSuccess) {
+        dense_workspace_free();
+        return fail(HFMOE_ERR_OUT_OF_MEMORY, "dense MLP workspace (inter %d, %d tokens): %s", inter, tokens,
+                    hipGetErrorString(e));
+    }
+    w.inter = inter;
+    w.tokens = tokens;
+    return HFMOE_OK;
+}
+
+// Slice rows for the decode kernels: the routed expert size when it divides
+// inter, else the largest divisor of inter that is a multiple of 8 and at
+// most 4096, with at most kMaxSlots slices.
+static int dense_slice(int inter) {
+    const int I = g.cfg.I;
+    if (inter % I == 0 && inter / I <= kMaxSlots) return I;
+    for (int n = (inter + 4095) / 4096; n <= kMaxSlots; ++n)
+        if (inter % n == 0 && (inter / n) % 8 == 0) return inter / n;
+    return 0;
+}
+
+#define HF_CHECK_LAUNCH(expr, what)                      \
+    do {                                                 \
+        hipError_t e_ = (expr);                          \
+        prof_end(p, s);                                  \
+        if (e_ != hipSuccess) return fail_hip(e_, what); \
+    } while (0)
+
+int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t s) {
+    const Cfg& c = g.cfg;
+    DenseWorkspace& w = g.dws;
+    Pending p;
+    const bool gemm = T > 1 && w.hh && c.d % kGemmTileK == 0 && L.dense_inter % kGemmTileK == 0;
+    if (!gemm) {
+        Cfg cd = c;
+        cd.k = 0;
+        cd.I = L.dense_slice;
+        cd.n_shared = L.dense_inter / L.dense_slice;
+        for (int t = 0; t < T; ++t) {
+            const float* xt = x + (size_t)t * c.d;
+            float* ot = out + (size_t)t * c.d;
+            prof_begin(p, "dense_gateup", s);
+            HF_CHECK_LAUNCH(launch_gateup_t1(xt, L.dev, cd, nullptr, nullptr, nullptr, w.h1, cd.n_shared,
+                                             gu_blocks(), s),
+                            "dense gate/up launch");
+            prof_begin(p, "dense_down", s);
+            HF_CHECK_LAUNCH(launch_down_t1(w.h1, L.dev, cd, nullptr, nullptr, nullptr, ot, cd.n_shared,
+                                           dn_blocks(), s),
+                            "dense down launch");
+        }
+        return HFMOE_OK;
+    }
+    GroupedWorkspace& gw = g.gws;
+    const int TR = T >= 192 ? 256 : kGemmTileRows;
+    const int I = L.dense_inter;
+    prof_begin(p, "split_x", s);
+    HF_CHECK_LAUNCH(launch_split_bf16(x, gw.xh, gw.xl, (size_t)T * c.d, gw.lo_flag, s), "split x");
+    GemmArgs gu{};
+    gu.K = c.d;
+    gu.N = I;
+    gu.tile_rows = TR;
+    gu.tile_cols = TR;
+    gu.n_tiles = (I + TR / 2 - 1) / (TR / 2);
+    gu.m_tiles = (T + TR - 1) / TR;
+    gu.rows_total = T;
+    gu.a_hi = gw.xh;
+    gu.a_lo = gw.xl;
+    gu.a_lo_flag = gw.lo_flag;
+    gu.b_fixed0 = L.dev.sg;
+    gu.b_fixed1 = L.dev.su;
+    gu.b_ld = c.d;
+    gu.h_hi = w.hh;
+    gu.h_lo = w.hl;
+    gu.ksplit = 1;
+    prof_begin(p, "dense_gateup_gemm", s);
+    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "dense gate/up gemm");
+    GemmArgs dn{};
+    dn.K = I;
+    dn.N = c.d;
+    dn.tile_rows = TR;
+    dn.tile_cols = TR;
+    dn.n_tiles = (c.d + TR - 1) / TR;
+    dn.m_tiles = (T + TR - 1) / TR;
+    dn.rows_total = T;
+    dn.a_hi = w.hh;
+    dn.a_lo = w.hl;
+    dn.b_fixed0 = L.dev.sd;
+    dn.b_ld = I;
+    dn.out_f32 = out;
+    dn.ksplit = 1;
+    prof_begin(p, "dense_down_gemm", s);
+    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, dn, gemm_blocks(TR), s), "dense down gemm");
+    return HFMOE_OK;
+}
+
+}  // namespace hf
+
+using namespace hf;
+
+extern "C" {
+
+int hfmoe_register_dense_layer(int layer, const hfmoe_dense_weights* w) {
+    int rc = require_cfg();
+    if (rc) return rc;
+    if (!w || !w->gate_dev || !w->up_dev || !w->down_dev)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: dense gate, up and down weights are required", layer);
+    const int inter = w->intermediate;
+    const int slice = inter > 0 && inter % 8 == 0 ? dense_slice(inter) : 0;
+    if (!slice)
+        return fail(HFMOE_ERR_UNSUPPORTED, "layer %d: dense intermediate %d must be a positive multiple of 8 "
+                    "splitting into at most %d slices of at most 4096 rows", layer, inter, kMaxSlots);
+    if ((size_t)inter * sizeof(float) > 160 * 1024)
+        return fail(HFMOE_ERR_UNSUPPORTED, "layer %d: dense intermediate %d FP32 activations exceed LDS", layer, inter);
+    rc = dense_workspace_reserve(inter);
+    if (rc) return rc;
+    auto it = g.layers.find(layer);
+    if (it != g.layers.end() && it->second.etab_dev) hipFree(it->second.etab_dev);
+    LayerState st;
+    st.dense = true;
+    st.dense_inter = inter;
+    st.dense_slice = slice;
+    st.dev.sg = w->gate_dev;
+    st.dev.su = w->up_dev;
+    st.dev.sd = w->down_dev;
+    st.norm_w = w->post_attention_norm_dev;
+    g.layers[layer] = st;
+    return HFMOE_OK;
+}
+
+int hfmoe_dense_mlp_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream) {
+    int rc = require_cfg();
+    if (rc) return rc;
+    auto it = g.layers.find(layer);
+    if (it == g.layers.end() || !it->second.dense)
+        return fail(HFMOE_ERR_NOT_REGISTERED, "layer %d is not a registered dense layer", layer);
+    if (T < 0 || T > g.max_tokens)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "T=%d outside 0..max_tokens=%d", T, g.max_tokens);
+    if (T == 0) return HFMOE_OK;
+    if (!x_dev || !out_dev) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null activation pointer");
+    if ((reinterpret_cast<uintptr_t>(x_dev) | reinterpret_cast<uintptr_t>(out_dev)) & 15)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
+    return dense_forward(it->second, x_dev, T, out_dev, pick_stream(stream));
+}
+
+}  // extern "C"

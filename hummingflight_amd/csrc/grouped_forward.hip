@@ -36,7 +36,7 @@ static int router_ksplit(int T) {
 
 // Persistent grid: two 4-wave workgroups per CU (128-row tiles) or one
 // workgroup per CU (256-row tiles).
-static int gemm_blocks(int tile_rows) {
+int gemm_blocks(int tile_rows) {
     return env_int("HFMOE_GEMM_BLOCKS", tile_rows == 256 ? g.num_cus : g.num_cus * 2);
 }
 

@@ -53,6 +53,21 @@ struct LayerState {
     const uint16_t** etab_dev = nullptr;
     std::vector<const uint16_t*> host_experts;  // 3*E as registered
     const uint16_t* norm_w = nullptr;
+    // Dense MLP layer: dev.sg / su / sd hold its gate, up and down matrices
+    // ([inter, d], [inter, d], [d, inter]), multiplied as dense_inter / dense_slice
+    // slices of dense_slice rows by the decode kernels.
+    bool dense = false;
+    int dense_inter = 0;
+    int dense_slice = 0;
+};
+
+// Buffers of the dense-MLP layers (sized for the largest registered inter).
+struct DenseWorkspace {
+    float* h1 = nullptr;     // [inter] T = 1 intermediate
+    uint16_t* hh = nullptr;  // [max_tokens, inter] h hi (multi-token path)
+    uint16_t* hl = nullptr;  // [max_tokens, inter] h lo
+    int inter = 0;
+    int tokens = 0;
 };
 
 struct Pending {
@@ -95,6 +110,7 @@ struct State {
     std::map<int, LayerState> layers;
     Workspace ws;
     GroupedWorkspace gws;
+    DenseWorkspace dws;
     StreamPool pool;
     StreamPolicyOptions stream_opt;   // kept across hfmoe_configure
     // profiling / telemetry
@@ -131,6 +147,10 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
                     const hfmoe_route_debug* dbg);
 int grouped_workspace_alloc();
 void grouped_workspace_free();
+int gemm_blocks(int tile_rows);
+// dense.hip
+int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t s);
+void dense_workspace_free();
 // streamed.hip
 int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hipStream_t s,
                         const hfmoe_route_debug* dbg);

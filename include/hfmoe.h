@@ -112,9 +112,24 @@ int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out
                             void* stream, const hfmoe_route_debug* dbg);
 /* The moeLayer contract itself: one token, host FP32 buffers, synchronous. */
 int hfmoe_moe_layer(int layer, const float* input_host, float* output_host);
-/* h_dev[T, hidden] += MoE(RMSNorm(h_dev)) -- the MoE half of a decoder layer
- * (glm_forward.cpp:785-796). */
+/* h_dev[T, hidden] += MLP(RMSNorm(h_dev)) -- the MLP half of a decoder layer
+ * (glm_forward.cpp:785-796): the MoE block, or the dense MLP for a layer
+ * registered with hfmoe_register_dense_layer. */
 int hfmoe_mlp_block(int layer, float* h_dev, int32_t T, void* stream);
+
+/* ---- dense MLP layers (the first first_k_dense_replace layers, config.h:53;
+ *      GLMForward::denseMlp, glm_forward.cpp:410-432) ---- */
+typedef struct hfmoe_dense_weights {
+    const uint16_t* gate_dev;  /* mlp.gate_proj.weight [inter, hidden] BF16 */
+    const uint16_t* up_dev;    /* mlp.up_proj.weight   [inter, hidden] */
+    const uint16_t* down_dev;  /* mlp.down_proj.weight [hidden, inter] */
+    const uint16_t* post_attention_norm_dev;  /* [hidden] or NULL (hfmoe_mlp_block) */
+    int32_t intermediate;      /* intermediateSize (config.h:16) */
+    int32_t reserved;
+} hfmoe_dense_weights;
+int hfmoe_register_dense_layer(int layer, const hfmoe_dense_weights* w);
+/* out_dev[T, hidden] = Wd.(silu(Wg.x) * (Wu.x)), FP32 in and out. */
+int hfmoe_dense_mlp_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
 
 /* ---- per-expert plugin surface (cuda_backend.h:64-90) ---- */
 int hfmoe_expert_cache_config(int capacity, int staging_depth); /* gpuExpertCacheConfig */
@@ -218,6 +233,10 @@ int hfmoe_checkpoint_tensor(const hfmoe_checkpoint* ck, const char* name, hfmoe_
  * expert as [gate | up | down] (scheduler.cpp:437-471) -- and registers the
  * layer.  The checkpoint owns these copies. */
 int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts_location);
+/* model.layers.<layer>.mlp.{gate,up,down}_proj.weight (+ post_attention_layernorm)
+ * of a dense layer to HBM, intermediate size from the tensors; registers it
+ * with hfmoe_register_dense_layer. */
+int hfmoe_checkpoint_load_dense_layer(hfmoe_checkpoint* ck, int layer);
 /* Unregisters the layers loaded from ck, frees their copies and the index. */
 void hfmoe_checkpoint_close(hfmoe_checkpoint* ck);
 

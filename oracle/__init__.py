@@ -123,6 +123,11 @@ def ref() -> C.CDLL | None:
                                           C.c_void_p, C.c_void_p, C.c_int, C.POINTER(C.c_double)]
         R.ref_rmsnorm.restype = C.c_int
         R.ref_rmsnorm.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        R.ref_dense_mlp.restype = C.c_int
+        R.ref_dense_mlp.argtypes = [C.c_char_p] + [C.c_void_p] * 3 + [C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        R.ref_lm_head.restype = C.c_int
+        R.ref_lm_head.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float,
+                                  C.c_void_p, C.c_void_p, C.POINTER(C.c_int)]
         _ref = R
     return _ref
 
@@ -203,6 +208,27 @@ def rmsnorm(w: np.ndarray | None, x: np.ndarray, eps: float) -> np.ndarray:
     wa = None if w is None else np.ascontiguousarray(w, np.uint16)
     lib().orc_rmsnorm(_p(wa), _p(x), len(x), eps)
     return x
+
+
+def dense_mlp(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray, hidden: int,
+              inter: int) -> np.ndarray:
+    """GLMForward::denseMlp (glm_forward.cpp:410-432): the expert SwiGLU with the
+    dense intermediate size (same serial GEMVs, same SiLU association)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(hidden, np.float32)
+    scratch = np.zeros(3 * inter, np.float32)
+    lib().orc_expert_ffn(_p(gate), _p(up), _p(down), _p(x), _p(y), hidden, inter, _p(scratch))
+    return y
+
+
+def lm_head(W: np.ndarray, norm: np.ndarray | None, h: np.ndarray, vocab: int, eps: float):
+    """GLMForward::lmHeadAndSample (glm_forward.cpp:663-731): final RMSNorm (the
+    rmsNorm formula with the norm weight widened to FP32), serial dot product per
+    vocabulary row (dotBf16F32, :67-92), greedy argmax taking the first maximum.
+    Returns (logits, best)."""
+    xn = rmsnorm(norm, h, eps)
+    logits = gemv(np.ascontiguousarray(W, np.uint16).reshape(vocab, -1), xn)
+    return logits, int(np.argmax(logits))
 
 
 # ------------------------------------------------------------ MoE layer ----

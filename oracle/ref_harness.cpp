@@ -47,6 +47,24 @@ struct RmsNormTag {
 };
 template struct Expose<RmsNormTag, &glm::GLMForward::rmsNorm>;
 
+struct DenseMlpTag {
+    using type = void (glm::GLMForward::*)(const glm::LayerWeights&, const float*, float*);
+    friend type get(DenseMlpTag);
+};
+template struct Expose<DenseMlpTag, &glm::GLMForward::denseMlp>;
+
+struct LmHeadTag {
+    using type = int (glm::GLMForward::*)(const float*, std::vector<float>*);
+    friend type get(LmHeadTag);
+};
+template struct Expose<LmHeadTag, &glm::GLMForward::lmHeadAndSample>;
+
+struct FinalNormTag {
+    using type = std::vector<float> glm::GLMForward::*;
+    friend type get(FinalNormTag);
+};
+template struct Expose<FinalNormTag, &glm::GLMForward::finalNorm_>;
+
 bool writeAt(int fd, const void* src, size_t bytes, uint64_t off) {
     const char* p = static_cast<const char*>(src);
     while (bytes > 0) {
@@ -234,6 +252,80 @@ int ref_rmsnorm(const char* path, const uint16_t* w, float* x, int n, float eps)
     }
     if (w) ::unlink(path);
     return 0;
+}
+
+// GLMForward::denseMlp (src/model/glm_forward.cpp:410-432): gate, up and down
+// [inter, hidden] / [inter, hidden] / [hidden, inter] via a scratch file.
+int ref_dense_mlp(const char* path, const uint16_t* gate, const uint16_t* up, const uint16_t* down,
+                  int hidden, int inter, const float* x, float* out) {
+    const uint64_t B = uint64_t(hidden) * uint64_t(inter) * 2;
+    int fd = ::open(path, O_CREAT | O_TRUNC | O_RDWR, 0600);
+    if (fd < 0) return -1;
+    bool ok = writeAt(fd, gate, B, 0) && writeAt(fd, up, B, B) && writeAt(fd, down, B, 2 * B);
+    ::close(fd);
+    if (!ok) {
+        ::unlink(path);
+        return -2;
+    }
+    int rc = 0;
+    {
+        glm::WeightIndex idx;
+        idx.config.hiddenSize = hidden;
+        idx.config.intermediateSize = inter;
+        glm::LayerWeights lw;
+        const std::string p(path);
+        lw.mlpGate = loc(p, 0, B, {inter, hidden}, "BF16");
+        lw.mlpUp = loc(p, B, B, {inter, hidden}, "BF16");
+        lw.mlpDown = loc(p, 2 * B, B, {hidden, inter}, "BF16");
+        if (!idx.getShardView(p)) {
+            rc = -3;
+        } else {
+            glm::GLMForward fwd(idx);
+            (fwd.*get(DenseMlpTag()))(lw, x, out);
+        }
+    }
+    ::unlink(path);
+    return rc;
+}
+
+// GLMForward::lmHeadAndSample (src/model/glm_forward.cpp:663-731): final
+// RMSNorm with the norm weight (finalNorm_, filled as init() does from
+// model.norm.weight, :135-148), logits over the vocabulary, greedy argmax.
+// lm_head [vocab, hidden] via a scratch file; norm NULL means all ones.
+int ref_lm_head(const char* path, const uint16_t* lm_head, const uint16_t* norm, int hidden, int vocab,
+                float eps, const float* h, float* logits, int* best) {
+    const uint64_t B = uint64_t(hidden) * uint64_t(vocab) * 2;
+    int fd = ::open(path, O_CREAT | O_TRUNC | O_RDWR, 0600);
+    if (fd < 0) return -1;
+    bool ok = writeAt(fd, lm_head, B, 0);
+    ::close(fd);
+    if (!ok) {
+        ::unlink(path);
+        return -2;
+    }
+    int rc = 0;
+    {
+        glm::WeightIndex idx;
+        idx.config.hiddenSize = hidden;
+        idx.config.vocabSize = vocab;
+        idx.config.rmsNormEps = eps;
+        const std::string p(path);
+        idx.lmHead = loc(p, 0, B, {vocab, hidden}, "BF16");
+        if (!idx.getShardView(p)) {
+            rc = -3;
+        } else {
+            glm::GLMForward fwd(idx);
+            std::vector<float>& fn = fwd.*get(FinalNormTag());
+            fn.assign(size_t(hidden), 1.0f);
+            if (norm)
+                for (int i = 0; i < hidden; ++i) fn[size_t(i)] = glm::BFloat16(norm[i]).toF32();
+            std::vector<float> lg;
+            *best = (fwd.*get(LmHeadTag()))(h, &lg);
+            std::memcpy(logits, lg.data(), sizeof(float) * size_t(vocab));
+        }
+    }
+    ::unlink(path);
+    return rc;
 }
 
 }  // extern "C"

@@ -5,7 +5,8 @@ built from its sources by `make -C oracle ref`).  Every vector below is an
 output of the reference's functions -- gemv_bf16_f32 (cpu_kernels.cpp:43-94),
 sigmoid_f32 (moe_router.h:19-21), topKScores (moe_router.h:29-57),
 BFloat16::fromF32 (dtype_bf16.h:27-33), GLMForward::rmsNorm
-(glm_forward.cpp:185-197) and GLMForward::moeLayer (glm_forward.cpp:509-661) --
+(glm_forward.cpp:185-197), GLMForward::moeLayer (glm_forward.cpp:509-661),
+GLMForward::denseMlp (:410-432) and GLMForward::lmHeadAndSample (:663-731) --
 on inputs from the seeded generator, so the fixtures hold seeds, a few inputs
 and the reference's outputs, never reference source.
 
@@ -108,6 +109,45 @@ def main() -> None:
                            "token": t, "idx": idx.tolist(), "w": bits(w), "out": bits(ro)})
         L.experts.clear()
     g["moe_layer"] = layers
+
+    # Dense MLP (GLMForward::denseMlp, glm_forward.cpp:410-432): a small shape
+    # and GLM-5.2's (hidden 6144, intermediate 12288), one seeded token each.
+    dense = []
+    for i, (H, I) in enumerate([(512, 1536), (6144, 12288)]):
+        seed = 8000 + i
+        gw = O.fill_bf16(I * H, seed, 1, 0.0, 0.02)
+        uw = O.fill_bf16(I * H, seed, 2, 0.0, 0.02)
+        dw = O.fill_bf16(H * I, seed, 3, 0.0, 0.02)
+        x = O.fill_f32(H, seed, 4, 0.0, 1.0)
+        out = np.zeros(H, np.float32)
+        if R.ref_dense_mlp(b"/tmp/hf_golden_dense.bin", gw.ctypes.data, uw.ctypes.data, dw.ctypes.data, H, I,
+                           x.ctypes.data, out.ctypes.data):
+            raise SystemExit("ref_dense_mlp failed")
+        dense.append({"hidden": H, "inter": I, "seed": seed, "w_std": 0.02, "out": bits(out)})
+    g["dense_mlp"] = dense
+
+    # LM head (GLMForward::lmHeadAndSample, glm_forward.cpp:663-731): final norm,
+    # logits, greedy argmax; GLM-5.2's vocabulary (154880) at hidden 6144 and a
+    # small one.  The fixture keeps the argmax, the ten largest logits and 64
+    # seeded samples.
+    import ctypes as C
+    lm = []
+    for i, (H, V) in enumerate([(512, 1000), (6144, 154880)]):
+        seed = 9000 + i
+        W = O.fill_bf16(V * H, seed, 1, 0.0, 0.02)
+        nw = O.fill_bf16(H, seed, 2, 1.0, 0.05)
+        h = O.fill_f32(H, seed, 3, 0.0, 1.0)
+        lg = np.zeros(V, np.float32)
+        best = C.c_int()
+        if R.ref_lm_head(b"/tmp/hf_golden_lm.bin", W.ctypes.data, nw.ctypes.data, H, V, 1e-5, h.ctypes.data,
+                         lg.ctypes.data, C.byref(best)):
+            raise SystemExit("ref_lm_head failed")
+        top = np.argsort(-lg, kind="stable")[:10]
+        sample = np.random.default_rng(seed).choice(V, 64, replace=False)
+        lm.append({"hidden": H, "vocab": V, "seed": seed, "eps": 1e-5, "best": best.value,
+                   "top": top.tolist(), "top_bits": bits(lg[top]), "sample": sample.tolist(),
+                   "sample_bits": bits(lg[sample])})
+    g["lm_head"] = lm
 
     path = os.path.join(OUT, "reference_vectors.json")
     with open(path, "w") as f:

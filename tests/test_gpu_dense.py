@@ -1,0 +1,135 @@
+"""Dense MLP layers (GLMForward::denseMlp) against the oracle.
+
+The oracle's dense_mlp is pinned bit-exact to the reference's own denseMlp
+(tests/test_oracle.py).  Here the library's decode path (T = 1: the expert
+GEMVs over inter / slice slices) and multi-token path (one-group grouped GEMM,
+128- and 256-row tiles) must agree with it within 1e-2 relative + 2e-3
+absolute, at a small shape and at GLM-5.2's (hidden 6144, intermediate 12288);
+the RMSNorm + residual block and a dense layer loaded from a checkpoint too.
+"""
+import ctypes as C
+import json
+
+import numpy as np
+import pytest
+
+import oracle as O
+from hummingflight_amd import capi, synth
+from moe_harness import assert_close
+from safetensors_io import write_shard
+
+pytestmark = pytest.mark.gpu
+
+
+class Dense:
+    """A seeded dense layer on the device and its host copy."""
+
+    def __init__(self, hidden, inter, seed, layer=0, with_norm=True):
+        self.hidden, self.inter, self.layer = hidden, inter, layer
+        n = hidden * inter
+        self.host = [O.fill_bf16(n, seed, 100 + i, 0.0, 0.02) for i in range(3)]
+        self.norm = O.fill_bf16(hidden, seed, 103, 1.0, 0.05) if with_norm else None
+        self.dev = [capi.DeviceBuffer(2 * n) for _ in range(3)]
+        for i, b in enumerate(self.dev):
+            synth.fill_bf16(b.ptr, n, seed, 100 + i, 0.0, 0.02)
+        self.norm_dev = None
+        if with_norm:
+            self.norm_dev = capi.DeviceBuffer(2 * hidden)
+            synth.fill_bf16(self.norm_dev.ptr, hidden, seed, 103, 1.0, 0.05)
+        w = capi.DenseWeights(self.dev[0].ptr, self.dev[1].ptr, self.dev[2].ptr,
+                              self.norm_dev.ptr if self.norm_dev else None, inter, 0)
+        capi.call("hfmoe_register_dense_layer", layer, C.byref(w))
+
+    def ref(self, x):
+        return O.dense_mlp(self.host[0], self.host[1], self.host[2], x, self.hidden, self.inter)
+
+    def forward(self, x):
+        T = x.shape[0]
+        xd = capi.DeviceBuffer.of(x)
+        out = capi.DeviceBuffer(x.nbytes)
+        capi.call("hfmoe_dense_mlp_forward", self.layer, xd.ptr, T, out.ptr, None)
+        capi.call("hfmoe_synchronize")
+        y = out.download(np.float32, x.size).reshape(x.shape)
+        xd.free()
+        out.free()
+        return y
+
+    def free(self):
+        for b in self.dev + ([self.norm_dev] if self.norm_dev else []):
+            b.free()
+
+
+def configure(hidden, inter, n_experts, max_tokens):
+    shape = synth.LayerShape(hidden=hidden, inter=inter, n_experts=n_experts, top_k=8, n_group=8, topk_group=4)
+    capi.call("hfmoe_configure", shape.config(max_tokens=max_tokens))
+
+
+def test_dense_small_decode_and_batches(hf):
+    H, I_moe, I = 1024, 512, 3072
+    configure(H, I_moe, 64, 300)
+    L = Dense(H, I, seed=31)
+    rng = np.random.default_rng(31)
+    x1 = rng.standard_normal((1, H)).astype(np.float32)
+    y1 = L.forward(x1)
+    assert_close(y1[0], L.ref(x1[0]), "T=1")
+    for T in (5, 300):  # 128-row and 256-row tiles
+        x = rng.standard_normal((T, H)).astype(np.float32)
+        y = L.forward(x)
+        for t in sorted({0, T // 2, T - 1}):
+            assert_close(y[t], L.ref(x[t]), f"T={T} token {t}")
+        # batch invariance against the decode path
+        assert_close(y[T - 1], L.forward(x[T - 1:T])[0], f"T={T} vs decode")
+    L.free()
+
+
+def test_dense_glm_shape(hf):
+    H, I = 6144, 12288
+    configure(H, 2048, 256, 8)
+    L = Dense(H, I, seed=32)
+    x = np.random.default_rng(32).standard_normal((8, H)).astype(np.float32)
+    y = L.forward(x)
+    for t in (0, 7):
+        assert_close(y[t], L.ref(x[t]), f"token {t}")
+    assert_close(L.forward(x[:1])[0], L.ref(x[0]), "decode")
+    L.free()
+
+
+def test_dense_block_and_moe_forward_rejected(hf):
+    H = 1024
+    configure(H, 512, 64, 4)
+    L = Dense(H, 2048, seed=33, layer=3)
+    x = np.random.default_rng(33).standard_normal(H).astype(np.float32)
+    h = capi.DeviceBuffer.of(x)
+    capi.call("hfmoe_mlp_block", 3, h.ptr, 1, None)
+    capi.call("hfmoe_synchronize")
+    want = x + L.ref(O.rmsnorm(L.norm, x, 1e-5))
+    assert_close(h.download(np.float32, H), want, "dense block")
+    assert capi.load().hfmoe_moe_forward(3, h.ptr, 1, h.ptr, None) == capi.ERR_INVALID_ARGUMENT
+    h.free()
+    L.free()
+
+
+def test_dense_layer_from_checkpoint(hf, tmp_path):
+    H, I = 1024, 2048
+    configure(H, 512, 64, 4)
+    gw, uw, dw = (O.fill_bf16(H * I, 34, 100 + i, 0.0, 0.02) for i in range(3))
+    norm = O.fill_bf16(H, 34, 103, 1.0, 0.05)
+    p = "model.layers.1."
+    write_shard(tmp_path / "model-00001-of-00001.safetensors",
+                {p + "mlp.gate_proj.weight": (gw, [I, H]), p + "mlp.up_proj.weight": (uw, [I, H]),
+                 p + "mlp.down_proj.weight": (dw, [H, I]), p + "post_attention_layernorm.weight": (norm, [H])})
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps(
+        {"weight_map": {k: "model-00001-of-00001.safetensors" for k in
+                        (p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight", p + "mlp.down_proj.weight",
+                         p + "post_attention_layernorm.weight")}}))
+    ck = C.c_void_p()
+    capi.call("hfmoe_checkpoint_open", str(tmp_path).encode(), C.byref(ck))
+    capi.call("hfmoe_checkpoint_load_dense_layer", ck, 1)
+    x = np.random.default_rng(34).standard_normal(H).astype(np.float32)
+    h = capi.DeviceBuffer.of(x)
+    capi.call("hfmoe_mlp_block", 1, h.ptr, 1, None)
+    capi.call("hfmoe_synchronize")
+    want = x + O.dense_mlp(gw, uw, dw, O.rmsnorm(norm, x, 1e-5), H, I)
+    assert_close(h.download(np.float32, H), want, "checkpoint dense block")
+    h.free()
+    capi.load().hfmoe_checkpoint_close(ck)

@@ -329,3 +329,66 @@ def test_moe_combine_linearity(oracle_lib):
     spec0 = O.LayerSpec(hidden=256, inter=128, n_experts=16, top_k=4, seed=21, n_shared=0)
     L0 = O.SyntheticLayer(spec0)
     assert np.array_equal(L0.combine(x, idx, np.zeros_like(w)), np.zeros(256, np.float32))
+
+
+# ------------------------------------------------------- dense MLP, LM head ----
+
+def dense_weights(O, c):
+    H, I, seed, sd = c["hidden"], c["inter"], c["seed"], c["w_std"]
+    return (O.fill_bf16(I * H, seed, 1, 0.0, sd), O.fill_bf16(I * H, seed, 2, 0.0, sd),
+            O.fill_bf16(H * I, seed, 3, 0.0, sd), O.fill_f32(H, seed, 4, 0.0, 1.0))
+
+
+@pytest.mark.parametrize("i", [0, 1], ids=["small", "glm_shape"])
+def test_dense_mlp_bit_exact_vs_reference(oracle_lib, golden, i):
+    O = oracle_lib
+    c = golden["dense_mlp"][i]
+    gw, uw, dw, x = dense_weights(O, c)
+    y = O.dense_mlp(gw, uw, dw, x, c["hidden"], c["inter"])
+    assert np.array_equal(y.view(np.uint32), np.array(c["out"], np.uint32))
+
+
+def test_dense_mlp_closed_forms(oracle_lib):
+    # Down is linear (doubling it doubles the output exactly); up = 0 gives 0;
+    # a 1x1 MLP is silu(g*x)*(u*x)*d in FP32.
+    O = oracle_lib
+    H, I = 64, 96
+    gw = O.fill_bf16(I * H, 3, 1, 0.0, 0.1)
+    uw = O.fill_bf16(I * H, 3, 2, 0.0, 0.1)
+    dw = O.fill_bf16(H * I, 3, 3, 0.0, 0.1)
+    x = O.fill_f32(H, 3, 4, 0.0, 1.0)
+    y = O.dense_mlp(gw, uw, dw, x, H, I)
+    d2 = O.f32_to_bf16(2.0 * O.bf16_to_f32(dw))
+    assert np.array_equal(O.dense_mlp(gw, uw, d2, x, H, I), 2.0 * y)
+    assert not np.any(O.dense_mlp(gw, np.zeros_like(uw), dw, x, H, I))
+    g1, u1, dn1 = (O.f32_to_bf16(np.array([v], np.float32)) for v in (0.75, -1.5, 2.0))
+    x1 = np.array([1.25], np.float32)
+    gv, uv = np.float32(0.75 * 1.25), np.float32(-1.5 * 1.25)
+    want = np.float32(np.float32(gv / np.float32(1.0 + np.exp(np.float32(-gv)))) * uv) * np.float32(2.0)
+    assert np.isclose(O.dense_mlp(g1, u1, dn1, x1, 1, 1)[0], want, rtol=1e-6)
+
+
+@pytest.mark.parametrize("i", [0, 1], ids=["small", "glm_vocab"])
+def test_lm_head_matches_reference(oracle_lib, golden, i):
+    O = oracle_lib
+    c = golden["lm_head"][i]
+    H, V, seed = c["hidden"], c["vocab"], c["seed"]
+    W = O.fill_bf16(V * H, seed, 1, 0.0, 0.02)
+    nw = O.fill_bf16(H, seed, 2, 1.0, 0.05)
+    h = O.fill_f32(H, seed, 3, 0.0, 1.0)
+    logits, best = O.lm_head(W, nw, h, V, c["eps"])
+    assert best == c["best"]
+    assert np.array_equal(logits[c["top"]].view(np.uint32), np.array(c["top_bits"], np.uint32))
+    assert np.array_equal(logits[c["sample"]].view(np.uint32), np.array(c["sample_bits"], np.uint32))
+
+
+def test_lm_head_argmax_closed_form(oracle_lib):
+    # Rows that are scaled copies of the normalised hidden state: the largest
+    # scale wins; on an exact tie the first row wins.
+    O = oracle_lib
+    H = 32
+    h = O.fill_f32(H, 5, 1, 0.0, 1.0)
+    xn = O.rmsnorm(None, h, 1e-5)
+    rows = np.stack([O.f32_to_bf16(s * xn) for s in (0.5, -1.0, 2.0, 1.0, 2.0)])
+    logits, best = O.lm_head(rows, None, h, 5, 1e-5)
+    assert best == 2 and logits[2] == logits[4]
