@@ -156,6 +156,63 @@ def run_decode(args) -> dict:
     return res
 
 
+def run_dense(args) -> dict:
+    """A dense MLP layer (GLM-5.2: hidden 6144, intermediate 12288; the first
+    three decoder layers) on --dense-tokens tokens."""
+    H, I, T = 6144, 12288, args.dense_tokens
+    shape = synth.LayerShape(**FULL)
+    capi.call("hfmoe_configure", shape.config(max_tokens=T))
+    w = [capi.DeviceBuffer(2 * H * I) for _ in range(3)]
+    for i, b in enumerate(w):
+        synth.fill_bf16(b.ptr, H * I, args.seed, 200 + i, 0.0, 0.02)
+    dw = capi.DenseWeights(w[0].ptr, w[1].ptr, w[2].ptr, None, I, 0)
+    capi.call("hfmoe_register_dense_layer", 0, C.byref(dw))
+    x = synth.make_x_dev(T, H, seed=args.seed)
+    out = capi.DeviceBuffer(T * H * 4)
+    fwd = capi.load().hfmoe_dense_mlp_forward
+
+    def step():
+        rc = fwd(0, x.ptr, T, out.ptr, None)
+        if rc:
+            capi.check(rc)
+
+    sec = time_steps(step, args.steps, args.warmup)
+    prof, sec_prof = profiled_pass(step, args.steps)
+    wbytes = 3 * H * I * 2
+    if T == 1:
+        algo = {"dense_gateup": (2 * H * I * 2 + H * 4 + I * 4, 2 * 2 * H * I),
+                "dense_down": (H * I * 2 + I * 4 + H * 4, 2 * H * I)}
+        dom_name = "dense_gateup"
+    else:
+        algo = {"dense_gateup_gemm": (2 * H * I * 2 + T * H * 2 + T * I * 4, 2 * 2 * T * H * I),
+                "dense_down_gemm": (H * I * 2 + T * I * 4 + T * H * 4, 2 * T * H * I),
+                "split_x": (T * H * 4 + T * H * 4, 0)}
+        dom_name = "dense_gateup_gemm"
+    kernels = kernel_table(prof, algo)
+    dom = kernels[dom_name]
+    nbytes, flops = algo[dom_name]
+    if flops / nbytes < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+    else:
+        roof = {"bound": "mfma", "kernel": dom_name, "achieved": dom["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None}
+    res = {
+        "value": T / sec,
+        "ms_per_step": sec * 1e3,
+        "config": {"workload": "dense_mlp", "tokens": T, "hidden": H, "intermediate": I,
+                   "weights": "HBM-resident BF16 ~N(0,0.02)"},
+        "roofline": roof,
+        "layer": {"weight_bytes": wbytes, "gbs": round(wbytes / sec / 1e9, 1),
+                  "tflops": round(2 * 3 * T * H * I / sec / 1e12, 2)},
+        "ms_per_step_with_kernel_events": sec_prof * 1e3,
+        "kernels": kernels,
+    }
+    for b in w + [x, out]:
+        b.free()
+    return res
+
+
 def grouped_algorithmic(shape: synth.LayerShape, T: int, U: int) -> dict[str, tuple[int, int]]:
     """(bytes, flops) each multi-token kernel must move / compute at least once.
 
@@ -495,6 +552,7 @@ METRICS = {
     "batched": "MoE-layer batched-decode tokens/s + HBM GB/s at d=6144, 256e top-8, T=64 Zipf(1.1)",
     "prefill": "MoE-layer prefill tokens/s + BF16 MFMA TFLOP/s at d=6144, 256e top-8, T=4096",
     "streamed": "8-layer streamed-expert decode tokens/s + PCIe GB/s at d=6144, 256e top-8",
+    "dense": "dense-MLP layer tokens/s + HBM GB/s at d=6144, intermediate 12288",
     "streamed_cached": "8-layer streamed-expert decode tokens/s with an HBM expert cache and next-layer "
                        "copy-ahead, correlated tokens, at d=6144, 256e top-8",
 }
@@ -506,7 +564,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "load", "copy"])
+                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "dense", "load",
+                             "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
@@ -516,6 +575,7 @@ def main() -> int:
                     help="streamed_cached: per-token deviation from the shared base input")
     ap.add_argument("--overlap-floor", type=float, default=0.5,
                     help="streamed: winner-overlap EMA below which next-layer copy-ahead is skipped")
+    ap.add_argument("--dense-tokens", type=int, default=1, help="dense: tokens per call")
     ap.add_argument("--load-experts", type=int, default=64,
                     help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -526,7 +586,7 @@ def main() -> int:
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
     defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
-                "streamed_cached": (30, 10), "load": (1, 0), "copy": (5, 0)}
+                "streamed_cached": (30, 10), "dense": (100, 10), "load": (1, 0), "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
     args.warmup = d_warm if args.warmup is None else args.warmup
@@ -537,6 +597,8 @@ def main() -> int:
         return 0
     if args.workload == "decode":
         res = run_decode(args)
+    elif args.workload == "dense":
+        res = run_dense(args)
     elif args.workload in ("streamed", "streamed_cached"):
         res = run_streamed(args, cached=args.workload == "streamed_cached")
     else:
