@@ -105,6 +105,8 @@ _SIGS = [
     ("hfmoe_moe_layer", C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
     ("hfmoe_mlp_block", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
     ("hfmoe_register_dense_layer", C.c_int, [C.c_int, C.POINTER(DenseWeights)]),
+    ("hfmoe_register_lm_head", C.c_int, [C.c_void_p, C.c_void_p, C.c_int32]),
+    ("hfmoe_lm_head", C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("hfmoe_dense_mlp_forward", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_expert_cache_config", C.c_int, [C.c_int, C.c_int]),
     ("hfmoe_expert_cache_shutdown", None, []),
@@ -137,6 +139,7 @@ _SIGS = [
     ("hfmoe_checkpoint_tensor", C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(TensorInfo)]),
     ("hfmoe_checkpoint_load_moe_layer", C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     ("hfmoe_checkpoint_load_dense_layer", C.c_int, [C.c_void_p, C.c_int]),
+    ("hfmoe_checkpoint_load_lm_head", C.c_int, [C.c_void_p]),
     ("hfmoe_checkpoint_close", None, [C.c_void_p]),
     ("hfmoe_stats", C.c_int, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
 ]

@@ -197,6 +197,7 @@ void hfmoe_shutdown(void) {
     free_workspace();
     grouped_workspace_free();
     dense_workspace_free();
+    lm_head_release();
     prof_drain();
     for (auto ev : g.event_pool) hipEventDestroy(ev);
     g.event_pool.clear();
@@ -262,6 +263,7 @@ int hfmoe_configure(const hfmoe_config* cfg) {
     g.layers.clear();
     stream_pool_release();
     dense_workspace_free();
+    lm_head_release();
     rc = alloc_workspace();
     if (rc) return rc;
     rc = grouped_workspace_alloc();

@@ -226,6 +226,7 @@ struct hfmoe_checkpoint {
     std::map<std::string, hf::TensorRef> tensors;
     hfmoe_safetensors_stats stats{};
     std::map<int, hf::LoadedLayer> loaded;
+    hf::LoadedLayer lm_head;  // lm_head.weight + model.norm.weight
 };
 
 namespace hf {
@@ -703,6 +704,49 @@ int hfmoe_checkpoint_load_dense_layer(hfmoe_checkpoint* ck, int layer) {
     return HFMOE_OK;
 }
 
+int hfmoe_checkpoint_load_lm_head(hfmoe_checkpoint* ck) {
+    int rc = require_cfg();
+    if (rc) return rc;
+    if (!ck) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null checkpoint");
+    const int64_t d = g.cfg.d;
+    auto it = ck->tensors.find("lm_head.weight");
+    if (it == ck->tensors.end()) return fail(HFMOE_ERR_INVALID_ARGUMENT, "tensor lm_head.weight is missing");
+    const int64_t vocab = it->second.shape.empty() ? 0 : it->second.shape[0];
+    std::string err;
+    const TensorRef* w = find2(*ck, "lm_head.weight", vocab, d, "BF16", err);
+    const TensorRef* norm = nullptr;
+    if (w && ck->tensors.count("model.norm.weight")) norm = find2(*ck, "model.norm.weight", d, 0, "BF16", err);
+    if (!w || (ck->tensors.count("model.norm.weight") && !norm))
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "%s", err.c_str());
+    LoadedLayer L;
+    std::vector<CopyJob> jobs;
+    void* p[2] = {};
+    const TensorRef* src[2] = {w, norm};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        if (!src[i]) continue;
+        e = hipMalloc(&p[i], src[i]->bytes());
+        if (e == hipSuccess) {
+            L.dev.push_back(p[i]);
+            jobs.push_back({src[i]->data(), p[i], src[i]->bytes(), true});
+        }
+    }
+    if (e == hipSuccess) e = run_copies(jobs);
+    if (e != hipSuccess) {
+        for (void* q : L.dev) hipFree(q);
+        return fail_hip(e, "checkpoint lm head upload");
+    }
+    rc = hfmoe_register_lm_head(static_cast<const uint16_t*>(p[0]), static_cast<const uint16_t*>(p[1]),
+                                (int32_t)vocab);
+    if (rc) {
+        for (void* q : L.dev) hipFree(q);
+        return rc;
+    }
+    for (void* q : ck->lm_head.dev) hipFree(q);
+    ck->lm_head = std::move(L);
+    return HFMOE_OK;
+}
+
 void hfmoe_checkpoint_close(hfmoe_checkpoint* ck) {
     if (!ck) return;
     for (auto& kv : ck->loaded) {
@@ -716,6 +760,13 @@ void hfmoe_checkpoint_close(hfmoe_checkpoint* ck) {
         }
         for (void* p : kv.second.dev) hipFree(p);
         for (void* p : kv.second.host) hipHostFree(p);
+    }
+    if (!ck->lm_head.dev.empty()) {
+        if (g.lm.w == ck->lm_head.dev[0]) {
+            if (g.stream) hipStreamSynchronize(g.stream);
+            lm_head_release();
+        }
+        for (void* p : ck->lm_head.dev) hipFree(p);
     }
     delete ck;
 }

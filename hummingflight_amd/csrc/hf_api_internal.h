@@ -61,6 +61,15 @@ struct LayerState {
     int dense_slice = 0;
 };
 
+// The LM head (lm_head.hip): caller-owned weights, the library's partial
+// argmax buffer.
+struct LmHead {
+    const uint16_t* w = nullptr;     // [vocab, d]
+    const uint16_t* norm = nullptr;  // final RMSNorm weight [d] or null
+    int vocab = 0;
+    void* part = nullptr;            // per-block winners of the T = 1 GEMV
+};
+
 // Buffers of the dense-MLP layers (sized for the largest registered inter).
 struct DenseWorkspace {
     float* h1 = nullptr;     // [inter] T = 1 intermediate
@@ -111,6 +120,7 @@ struct State {
     Workspace ws;
     GroupedWorkspace gws;
     DenseWorkspace dws;
+    LmHead lm;
     StreamPool pool;
     StreamPolicyOptions stream_opt;   // kept across hfmoe_configure
     // profiling / telemetry
@@ -151,6 +161,8 @@ int gemm_blocks(int tile_rows);
 // dense.hip
 int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t s);
 void dense_workspace_free();
+// lm_head.hip
+void lm_head_release();
 // streamed.hip
 int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hipStream_t s,
                         const hfmoe_route_debug* dbg);

@@ -131,6 +131,14 @@ int hfmoe_register_dense_layer(int layer, const hfmoe_dense_weights* w);
 /* out_dev[T, hidden] = Wd.(silu(Wg.x) * (Wu.x)), FP32 in and out. */
 int hfmoe_dense_mlp_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
 
+/* ---- LM head (GLMForward::lmHeadAndSample, glm_forward.cpp:663-731) ---- */
+/* lm_head.weight [vocab, hidden] BF16 and model.norm.weight [hidden] (NULL:
+ * ones), both caller-owned HBM; replaces any earlier registration. */
+int hfmoe_register_lm_head(const uint16_t* lm_head_dev, const uint16_t* final_norm_dev, int32_t vocab);
+/* logits_dev[T, vocab] = lm_head . RMSNorm(h_dev[t]); token_dev[t] (optional)
+ * = first index of the largest logit (greedy sampling). */
+int hfmoe_lm_head(const float* h_dev, int32_t T, float* logits_dev, int32_t* token_dev, void* stream);
+
 /* ---- per-expert plugin surface (cuda_backend.h:64-90) ---- */
 int hfmoe_expert_cache_config(int capacity, int staging_depth); /* gpuExpertCacheConfig */
 void hfmoe_expert_cache_shutdown(void);                         /* gpuExpertCacheShutdown */
@@ -237,7 +245,9 @@ int hfmoe_checkpoint_load_moe_layer(hfmoe_checkpoint* ck, int layer, int experts
  * of a dense layer to HBM, intermediate size from the tensors; registers it
  * with hfmoe_register_dense_layer. */
 int hfmoe_checkpoint_load_dense_layer(hfmoe_checkpoint* ck, int layer);
-/* Unregisters the layers loaded from ck, frees their copies and the index. */
+/* lm_head.weight (+ model.norm.weight) to HBM; registers the LM head. */
+int hfmoe_checkpoint_load_lm_head(hfmoe_checkpoint* ck);
+/* Unregisters the layers (and LM head) loaded from ck, frees their copies and the index. */
 void hfmoe_checkpoint_close(hfmoe_checkpoint* ck);
 
 /* ---- telemetry (InferenceStats gpuActiveNs / pcieBytes,
