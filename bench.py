@@ -213,6 +213,47 @@ def run_dense(args) -> dict:
     return res
 
 
+def run_lm_head(args) -> dict:
+    """Final norm + LM head + greedy argmax at GLM-5.2's size (vocab 154880,
+    hidden 6144), one token."""
+    H, V = 6144, 154880
+    shape = synth.LayerShape(**FULL)
+    capi.call("hfmoe_configure", shape.config(max_tokens=1))
+    W = capi.DeviceBuffer(2 * V * H)
+    synth.fill_bf16(W.ptr, V * H, args.seed, 300, 0.0, 0.02)
+    norm = capi.DeviceBuffer(2 * H)
+    synth.fill_bf16(norm.ptr, H, args.seed, 301, 1.0, 0.05)
+    capi.call("hfmoe_register_lm_head", W.ptr, norm.ptr, V)
+    x = synth.make_x_dev(1, H, seed=args.seed)
+    lg = capi.DeviceBuffer(V * 4)
+    tok = capi.DeviceBuffer(4)
+    fwd = capi.load().hfmoe_lm_head
+
+    def step():
+        rc = fwd(x.ptr, 1, lg.ptr, tok.ptr, None)
+        if rc:
+            capi.check(rc)
+
+    sec = time_steps(step, args.steps, args.warmup)
+    prof, sec_prof = profiled_pass(step, args.steps)
+    algo = {"lm_head_gemv": (V * H * 2 + H * 4 + V * 4, 2 * V * H)}
+    kernels = kernel_table(prof, algo)
+    dom = kernels["lm_head_gemv"]
+    res = {
+        "value": 1.0 / sec,
+        "ms_per_step": sec * 1e3,
+        "config": {"workload": "lm_head_greedy", "tokens": 1, "hidden": H, "vocab": V,
+                   "weights": "HBM-resident BF16 ~N(0,0.02)"},
+        "roofline": {"bound": "hbm", "kernel": "lm_head_gemv", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "ms_per_step_with_kernel_events": sec_prof * 1e3,
+        "kernels": kernels,
+    }
+    for b in (W, norm, x, lg, tok):
+        b.free()
+    return res
+
+
 def grouped_algorithmic(shape: synth.LayerShape, T: int, U: int) -> dict[str, tuple[int, int]]:
     """(bytes, flops) each multi-token kernel must move / compute at least once.
 
@@ -553,6 +594,7 @@ METRICS = {
     "prefill": "MoE-layer prefill tokens/s + BF16 MFMA TFLOP/s at d=6144, 256e top-8, T=4096",
     "streamed": "8-layer streamed-expert decode tokens/s + PCIe GB/s at d=6144, 256e top-8",
     "dense": "dense-MLP layer tokens/s + HBM GB/s at d=6144, intermediate 12288",
+    "lm_head": "LM head + greedy argmax tokens/s + HBM GB/s at d=6144, vocab 154880",
     "streamed_cached": "8-layer streamed-expert decode tokens/s with an HBM expert cache and next-layer "
                        "copy-ahead, correlated tokens, at d=6144, 256e top-8",
 }
@@ -564,8 +606,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "dense", "load",
-                             "copy"])
+                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "dense", "lm_head",
+                             "load", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
@@ -586,7 +628,8 @@ def main() -> int:
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
     defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
-                "streamed_cached": (30, 10), "dense": (100, 10), "load": (1, 0), "copy": (5, 0)}
+                "streamed_cached": (30, 10), "dense": (100, 10), "lm_head": (100, 10), "load": (1, 0),
+                "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
     args.warmup = d_warm if args.warmup is None else args.warmup
@@ -599,6 +642,8 @@ def main() -> int:
         res = run_decode(args)
     elif args.workload == "dense":
         res = run_dense(args)
+    elif args.workload == "lm_head":
+        res = run_lm_head(args)
     elif args.workload in ("streamed", "streamed_cached"):
         res = run_streamed(args, cached=args.workload == "streamed_cached")
     else:

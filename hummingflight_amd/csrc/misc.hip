@@ -4,23 +4,50 @@
 
 namespace hf {
 
-// One block per token: r = 1/sqrt(sum(x^2)/n + eps); out = x*r*w (w BF16 or 1).
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ h,
-                                                      const uint16_t* __restrict__ w,
-                                                      float* __restrict__ out, int d, float eps) {
-    __shared__ float red[4];
+// One block of 1024 threads per token: r = 1/sqrt(sum(x^2)/n + eps);
+// out = x*r*w (w BF16 or 1).  Each thread loads its (at most two) float4
+// chunks once and keeps them in registers for the second pass, so a token
+// costs one round trip to memory, not two.
+constexpr int kNormThreads = 1024;
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ h,
+                                                               const uint16_t* __restrict__ w,
+                                                               float* __restrict__ out, int d, float eps) {
+    __shared__ float red[kNormThreads / 64];
     const float* x = h + (size_t)blockIdx.x * d;
     float* y = out + (size_t)blockIdx.x * d;
+    const bool vec = (d & 3) == 0;
+    float4 v[2];
     float sq = 0.0f;
-    for (int i = threadIdx.x; i < d; i += 256) sq = fmaf(x[i], x[i], sq);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = 4 * (threadIdx.x + j * kNormThreads);
+        v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (vec && i < d) v[j] = *reinterpret_cast<const float4*>(x + i);
+        sq = fmaf(v[j].x, v[j].x, sq);
+        sq = fmaf(v[j].y, v[j].y, sq);
+        sq = fmaf(v[j].z, v[j].z, sq);
+        sq = fmaf(v[j].w, v[j].w, sq);
+    }
+    if (!vec)
+        for (int i = threadIdx.x; i < d; i += kNormThreads) sq = fmaf(x[i], x[i], sq);
     sq = wave_sum(sq);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
     __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
     const float r = 1.0f / sqrtf(tot / (float)d + eps);
-    for (int i = threadIdx.x; i < d; i += 256) {
-        const float v = x[i] * r;
-        y[i] = w ? v * __uint_as_float((uint32_t)w[i] << 16) : v;
+    auto wt = [&](int i) { return w ? __uint_as_float((uint32_t)w[i] << 16) : 1.0f; };
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = 4 * (threadIdx.x + j * kNormThreads);
+            if (i < d)
+                *reinterpret_cast<float4*>(y + i) =
+                    make_float4(v[j].x * r * wt(i), v[j].y * r * wt(i + 1), v[j].z * r * wt(i + 2), v[j].w * r * wt(i + 3));
+        }
+    } else {
+        for (int i = threadIdx.x; i < d; i += kNormThreads) y[i] = x[i] * r * wt(i);
     }
 }
 
@@ -31,7 +58,8 @@ __global__ void add_inplace_kernel(float* __restrict__ dst, const float* __restr
 
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s) {
-    return launch(rmsnorm_kernel, dim3(T), dim3(256), 0, s, h, w, out, d, eps);
+    if (d > 8 * kNormThreads) return hipErrorInvalidValue;
+    return launch(rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, s, h, w, out, d, eps);
 }
 
 hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s) {
