@@ -7,9 +7,9 @@
 // maximum; its OpenMP merge of per-thread winners is the same unless two
 // threads hold exactly equal maxima).
 //
-// T = 1: a persistent GEMV.  Each wavefront keeps the normalised hidden state
-//   in registers (lane l holds elements 512j + 8l .. +7) and streams whole
-//   vocabulary rows, two at a time, 16-byte loads; lane 0 writes the logit and
+// T = 1: a persistent GEMV.  Each block stages the normalised hidden state in
+//   LDS; each wavefront streams whole vocabulary rows, two at a time, 16-byte
+//   loads (lane l: elements 512j + 8l .. +7); lane 0 writes the logit and
 //   keeps the wavefront's running winner, the block merges its four, and one
 //   small launch merges the blocks' winners (lowest row on equal values).
 // T > 1: the grouped GEMM (one group, fixed B = lm_head) writes the logits,
@@ -37,17 +37,13 @@ __global__ __launch_bounds__(kLmBlock) void lm_gemv_kernel(const uint16_t* __res
                                                            const float* __restrict__ x, int V, int K,
                                                            float* __restrict__ logits,
                                                            ArgMax* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) float xs[KCH * 512];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = gridDim.x * (kLmBlock / 64);
     const int gw = blockIdx.x * (kLmBlock / 64) + wave;
-    float xr[KCH][8];
-#pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-        const int k0 = j * 512 + lane * 8;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) xr[j][q] = k0 < K ? x[k0 + q] : 0.0f;
-    }
+    for (int i = threadIdx.x; i < KCH * 512; i += kLmBlock) xs[i] = i < K ? x[i] : 0.0f;
+    __syncthreads();
     float best = -INFINITY;
     int best_i = INT_MAX;
     for (int r0 = gw * RF; r0 < V; r0 += nwaves * RF) {
@@ -62,20 +58,32 @@ __global__ __launch_bounds__(kLmBlock) void lm_gemv_kernel(const uint16_t* __res
                 w[u][j] = k0 < K ? *reinterpret_cast<const u32x4*>(row + k0) : (u32x4){0, 0, 0, 0};
             }
         }
+        float acc[RF];
 #pragma unroll
-        for (int u = 0; u < RF; ++u) {
-            float acc = 0.0f;
+        for (int u = 0; u < RF; ++u) acc[u] = 0.0f;
+        // Re-read x from LDS for every row pair: an opaque offset keeps the
+        // compiler from hoisting the reads (and 96 registers) out of the loop.
+        int xo = lane * 8;
+        asm volatile("" : "+v"(xo));
 #pragma unroll
-            for (int j = 0; j < KCH; ++j) {
+        for (int j = 0; j < KCH; ++j) {
+            const float4 xa = *reinterpret_cast<const float4*>(xs + j * 512 + xo);
+            const float4 xb = *reinterpret_cast<const float4*>(xs + j * 512 + xo + 4);
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int u = 0; u < RF; ++u) {
                 const u32x4 v = w[u][j];
                 const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    acc = fmaf(__uint_as_float(ws[q] << 16), xr[j][2 * q], acc);
-                    acc = fmaf(__uint_as_float(ws[q] & 0xFFFF0000u), xr[j][2 * q + 1], acc);
+                    acc[u] = fmaf(__uint_as_float(ws[q] << 16), xv[2 * q], acc[u]);
+                    acc[u] = fmaf(__uint_as_float(ws[q] & 0xFFFF0000u), xv[2 * q + 1], acc[u]);
                 }
             }
-            const float dot = wave_sum(acc);
+        }
+#pragma unroll
+        for (int u = 0; u < RF; ++u) {
+            const float dot = wave_sum(acc[u]);
             const int r = r0 + u;
             if (r < V) {
                 if (lane == 0) logits[r] = dot;
@@ -151,8 +159,8 @@ static hipError_t launch_lm_gemv(const uint16_t* W, const float* x, int V, int K
     return hipErrorInvalidValue;
 }
 
-// Two 4-wave blocks per CU: the hidden state held in registers (96 VGPRs at
-// hidden 6144) leaves room for two wavefronts per SIMD.
+// Two 4-wave blocks per CU (two rows of loads in flight per wavefront take
+// ~176 registers at hidden 6144; more rows or blocks measured no faster).
 static int lm_grid() { return env_int("HFMOE_LM_BLOCKS", g.num_cus * 2); }
 
 void lm_head_release() {
