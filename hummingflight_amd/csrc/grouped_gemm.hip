@@ -368,10 +368,16 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
     }
 }
 
+// How the A operand's lo half is handled: kLoNone (A is BF16), kLoByFlag
+// (x: multiplied only when the device flag says some lo half is nonzero),
+// kLoAlways (h: always; the kernel is compiled for that path alone, which
+// also leaves it more registers).
+enum { kLoNone = 0, kLoByFlag = 1, kLoAlways = 2 };
+
 // WAVES = 4: 128-row tiles, two workgroups per CU; WAVES = 8: 256-row tiles
 // (one expert's rows in one tile at prefill sizes, so each weight tile
 // crosses the memory system once), one workgroup per CU.
-template <int EPI, bool LO, int WAVES>
+template <int EPI, int LOM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) BStage ring[];  // kRingBytes
     const int t = threadIdx.x;
@@ -379,13 +385,14 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<false>(a, m_tiles);
-    // The lo half is multiplied only when present (x that is BF16-valued has none).
-    const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
+    const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
 
     for (int li = r.begin; li < r.end; li += r.stride) {
         const int item = r.item(li);
-        if (use_lo)
-            gemm_item<EPI, LO, WAVES>(a, item, ring, t, wave);
+        if constexpr (LOM == kLoAlways)
+            gemm_item<EPI, true, WAVES>(a, item, ring, t, wave);
+        else if (LOM == kLoByFlag && use_lo)
+            gemm_item<EPI, LOM == kLoByFlag, WAVES>(a, item, ring, t, wave);
         else
             gemm_item<EPI, false, WAVES>(a, item, ring, t, wave);
         __syncthreads();  // all DMA landed and all ring reads done before the next item
@@ -567,18 +574,20 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WSta
     }
 }
 
-template <int EPI, bool LO>
+template <int EPI, int LOM>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) WStage wring[];  // kWideRingBytes
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
-    const bool use_lo = LO && (a.a_lo_flag ? (*a.a_lo_flag != 0u) : true);
+    const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
     for (int li = r.begin; li < r.end; li += r.stride) {
         const int item = r.item(li);
-        if (use_lo)
-            gemm_item_wide<EPI, LO>(a, item, wring, t, wave);
+        if constexpr (LOM == kLoAlways)
+            gemm_item_wide<EPI, true>(a, item, wring, t, wave);
+        else if (LOM == kLoByFlag && use_lo)
+            gemm_item_wide<EPI, LOM == kLoByFlag>(a, item, wring, t, wave);
         else
             gemm_item_wide<EPI, false>(a, item, wring, t, wave);
         __syncthreads();
@@ -645,41 +654,44 @@ __global__ void router_reduce_kernel(const float* __restrict__ part, int ksplit,
     scores[i] = score_pair(s, bias, i % E);
 }
 
-template <int EPI, bool LO, int WAVES>
+template <int EPI, int LOM, int WAVES>
 static hipError_t launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
     static bool raised = false;  // the ring exceeds the default 64 KB of dynamic LDS
     if (!raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<EPI, LO, WAVES>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_kernel<EPI, LOM, WAVES>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRingBytes);
         if (e != hipSuccess) return e;
         raised = true;
     }
-    return launch(grouped_gemm_kernel<EPI, LO, WAVES>, dim3(blocks), dim3(64 * WAVES), (uint32_t)kRingBytes, s, a);
+    return launch(grouped_gemm_kernel<EPI, LOM, WAVES>, dim3(blocks), dim3(64 * WAVES), (uint32_t)kRingBytes, s, a);
 }
 
-template <int EPI, bool LO>
+template <int EPI, int LOM>
 static hipError_t launch_gemm_wide(const GemmArgs& a, int blocks, hipStream_t s) {
     static bool raised = false;
     if (!raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel<EPI, LO>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel<EPI, LOM>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideRingBytes);
         if (e != hipSuccess) return e;
         raised = true;
     }
-    return launch(grouped_gemm_wide_kernel<EPI, LO>, dim3(blocks), dim3(512), (uint32_t)kWideRingBytes, s, a);
+    return launch(grouped_gemm_wide_kernel<EPI, LOM>, dim3(blocks), dim3(512), (uint32_t)kWideRingBytes, s, a);
+}
+
+template <int EPI, int LOM>
+static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
+    if (a.tile_rows == 256 && a.tile_cols == 256) return launch_gemm_wide<EPI, LOM>(a, blocks, s);
+    if (a.tile_cols != 128) return hipErrorInvalidValue;
+    if (a.tile_rows == 256) return launch_gemm<EPI, LOM, 8>(a, blocks, s);
+    if (a.tile_rows == 128) return launch_gemm<EPI, LOM, 4>(a, blocks, s);
+    return hipErrorInvalidValue;
 }
 
 template <int EPI>
 static hipError_t launch_epi(const GemmArgs& a, int blocks, hipStream_t s) {
-    const bool lo = a.a_lo != nullptr;
-    if (a.tile_rows == 256 && a.tile_cols == 256)
-        return lo ? launch_gemm_wide<EPI, true>(a, blocks, s) : launch_gemm_wide<EPI, false>(a, blocks, s);
-    if (a.tile_cols != 128) return hipErrorInvalidValue;
-    if (a.tile_rows == 256)
-        return lo ? launch_gemm<EPI, true, 8>(a, blocks, s) : launch_gemm<EPI, false, 8>(a, blocks, s);
-    if (a.tile_rows == 128)
-        return lo ? launch_gemm<EPI, true, 4>(a, blocks, s) : launch_gemm<EPI, false, 4>(a, blocks, s);
-    return hipErrorInvalidValue;
+    if (!a.a_lo) return launch_shape<EPI, kLoNone>(a, blocks, s);
+    if (a.a_lo_flag) return launch_shape<EPI, kLoByFlag>(a, blocks, s);
+    return launch_shape<EPI, kLoAlways>(a, blocks, s);
 }
 
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s) {
