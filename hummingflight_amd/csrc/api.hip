@@ -287,6 +287,7 @@ int hfmoe_register_layer(int layer, const hfmoe_layer_weights* w) {
         if (!w->experts[i]) return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: expert pointer %d is NULL", layer, i);
     auto it = g.layers.find(layer);
     if (it != g.layers.end() && it->second.etab_dev) hipFree(it->second.etab_dev);
+    g.pool.policy.forget_layer(layer);  // cached HBM copies hold the old weights
     LayerState st;
     st.location = w->experts_location;
     st.host_experts.assign(w->experts, w->experts + 3 * c.E);

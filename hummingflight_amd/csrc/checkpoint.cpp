@@ -750,9 +750,15 @@ int hfmoe_checkpoint_load_lm_head(hfmoe_checkpoint* ck) {
 void hfmoe_checkpoint_close(hfmoe_checkpoint* ck) {
     if (!ck) return;
     for (auto& kv : ck->loaded) {
-        // The layer's weights go with the checkpoint: unregister it first.
+        // The layer's weights go with the checkpoint: unregister it first --
+        // unless the layer id now holds another registration (after a
+        // reconfigure or an explicit register call), which is left alone.
         auto it = g.layers.find(kv.first);
-        if (it != g.layers.end()) {
+        const void* first = kv.second.dev.empty() ? nullptr : kv.second.dev[0];
+        const bool ours = it != g.layers.end() && first &&
+                          (it->second.dense ? it->second.dev.sg == first : it->second.dev.router == first);
+        if (ours) {
+            g.pool.policy.forget_layer(kv.first);
             if (g.stream) hipStreamSynchronize(g.stream);
             if (g.copy_stream) hipStreamSynchronize(g.copy_stream);
             if (it->second.etab_dev) hipFree(it->second.etab_dev);

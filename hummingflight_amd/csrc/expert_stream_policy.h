@@ -155,6 +155,23 @@ public:
         return s;
     }
 
+    // Drops every cached expert of `layer` (its weights were re-registered or
+    // unregistered) and the layer's routing history.  Slots become empty.
+    void forget_layer(int layer) {
+        for (int s = 0; s < slots(); ++s) {
+            if (key_[s] == kEmpty || (int)(uint32_t)(key_[s] >> 32) != layer) continue;
+            where_.erase(key_[s]);
+            unlink(s);
+            key_[s] = kEmpty;
+            protect_[s] = 0;
+            staged_[s] = used_[s] = 0;
+        }
+        last_topk_.erase(layer);
+        overlap_.erase(layer);
+        for (auto it = heat_.begin(); it != heat_.end();)
+            it = (int)(uint32_t)(it->first >> 32) == layer ? heat_.erase(it) : std::next(it);
+    }
+
     // Soft boost: most recent, and survives `cycles` eviction sweeps.
     void boost(uint64_t key, int cycles) {
         const int s = find(key);

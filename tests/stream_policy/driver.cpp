@@ -6,6 +6,7 @@
 //   reset SLOTS
 //   opt PREFETCH EMA EMA_ALPHA OVERLAP_FLOOR OVERLAP_ALPHA
 //   call LAYER NEXT_STREAMED K E1 .. EK
+//   forget LAYER  (the layer was re-registered: drop its cached experts)
 // stdout per call: "L s0 c0 s1 c1 ..." (slot, copy flag per selected expert),
 // then "S e0 s0 e1 s1 ..." (copied-ahead expert and slot); at the end the
 // counters in the order of hfmoe_stream_counters.
@@ -36,6 +37,10 @@ int main() {
             in >> pf >> ema >> p.opt.ema_alpha >> p.opt.overlap_floor >> p.opt.overlap_alpha;
             p.opt.prefetch = pf != 0;
             p.opt.ema_predictor = ema != 0;
+        } else if (cmd == "forget") {
+            int layer = 0;
+            in >> layer;
+            p.forget_layer(layer);
         } else if (cmd == "call") {
             int layer = 0, next = 0, k = 0;
             in >> layer >> next >> k;

@@ -118,3 +118,17 @@ def test_checkpoint_missing_or_misshaped_tensor_is_named(hf, ckpt_dir, tmp_path)
     assert L.hfmoe_checkpoint_load_moe_layer(ck, LAYER, capi.EXPERTS_DEVICE) == capi.ERR_INVALID_ARGUMENT
     assert b"expected BF16 [32,2048]" in L.hfmoe_last_error()
     L.hfmoe_checkpoint_close(ck)
+
+
+def test_close_leaves_a_later_registration_alone(hf, ckpt_dir):
+    # Load layer 2 from the checkpoint, then register other weights under the
+    # same id: closing the checkpoint must not unregister (or free) those.
+    path, ref, norm = ckpt_dir
+    ck = load(path, capi.EXPERTS_DEVICE)
+    shape = synth.LayerShape(n_group=4, topk_group=2, **DIMS)
+    other = synth.DeviceLayer(shape, layer=LAYER, seed=SEED + 1)
+    capi.load().hfmoe_checkpoint_close(ck)
+    x = np.random.default_rng(7).standard_normal((1, DIMS["hidden"])).astype(np.float32)
+    ref2 = O.SyntheticLayer(O.LayerSpec(n_group=4, topk_group=2, seed=SEED + 1, layer=LAYER, **DIMS))
+    check(ref2, x, forward(1, x))
+    other.free()

@@ -114,3 +114,40 @@ def test_streamed_cache_and_copy_ahead(hf, opts):
     set_options(prefetch_next_layer=1, ema_predictor=0, ema_alpha=0.1, overlap_floor=0.5, overlap_alpha=0.5)
     for L in layers:
         L.free()
+
+
+def test_reregistered_streamed_layer_drops_cached_experts(hf):
+    # The same token through layer 0 registered with one weight set, then
+    # re-registered with another: the second output must be the second
+    # layer's, not a mix with experts cached from the first.
+    d, k = DIMS["hidden"], DIMS["top_k"]
+    shape = synth.LayerShape(n_group=4, topk_group=2, **DIMS)
+    cfg = shape.config(max_tokens=1)
+    cfg.vram_budget_bytes = 64 * 6 * d * DIMS["inter"]  # room for every expert
+    capi.call("hfmoe_configure", cfg)
+    x = np.random.default_rng(5).standard_normal((1, d)).astype(np.float32)
+    outs = []
+    for seed in (91, 92):
+        L = synth.DeviceLayer(shape, layer=0, seed=seed, experts_on_host=True)
+        got = run_chain_one(x, d, k, DIMS["n_experts"])
+        ref = O.SyntheticLayer(O.LayerSpec(n_group=4, topk_group=2, seed=seed, layer=0, **DIMS))
+        ridx, rw = ref.route(got["logits"])
+        assert got["idx"] == ridx.tolist()
+        assert_close(got["out"], ref.combine(x[0], ridx, rw), f"weights of seed {seed}")
+        outs.append((L, got))
+    assert read_counters()["misses"] == 2 * k  # both registrations copied their experts
+    for L, _ in outs:
+        L.free()
+
+
+def run_chain_one(x, d, k, E):
+    out, lg, idx, w = capi.DeviceBuffer(d * 4), capi.DeviceBuffer(E * 4), capi.DeviceBuffer(k * 4), capi.DeviceBuffer(k * 4)
+    dbg = capi.RouteDebug(lg.ptr, idx.ptr, w.ptr, None, None)
+    xd = capi.DeviceBuffer.of(x)
+    capi.call("hfmoe_moe_forward_debug", 0, xd.ptr, 1, out.ptr, None, C.byref(dbg))
+    capi.call("hfmoe_synchronize")
+    res = dict(out=out.download(np.float32, d), logits=lg.download(np.float32, E),
+               idx=idx.download(np.int32, k).tolist())
+    for b in (out, lg, idx, w, xd):
+        b.free()
+    return res

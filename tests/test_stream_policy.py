@@ -164,3 +164,17 @@ def test_library_policy_matches_oracle(driver):
         assert len(got) == len(want), case
         for i, (g, w) in enumerate(zip(got, want)):
             assert g.strip() == w.strip(), f"case {case} line {i}: library {g!r} oracle {w!r}"
+
+
+def test_library_forget_layer_drops_only_that_layer(driver):
+    # Re-registering a layer's weights must not serve its old cached copies;
+    # the other layers' entries and slots stay (no counterpart in the
+    # reference, whose device cache is never re-keyed).
+    lines = ["opt 0 0 0.1 0.5 0.5", "reset 8", "call 0 0 2 1 2", "call 1 0 2 1 2", "forget 0",
+             "call 0 0 2 1 2", "call 1 0 2 1 2"]
+    r = subprocess.run([driver], input="\n".join(lines) + "\n", capture_output=True, text=True, check=True)
+    out = r.stdout.strip().split("\n")
+    assert out[0] == "L 0 1 1 1" and out[2] == "L 2 1 3 1"
+    assert out[4] == "L 0 1 1 1"  # layer 0 copied again into its freed slots
+    assert out[6] == "L 2 0 3 0"  # layer 1 still resident
+    assert out[-1].split()[1:4] == ["8", "2", "6"]  # lookups, hits, misses
