@@ -106,6 +106,15 @@ _SIGS = [
     ("hfmoe_mlp_block", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
     ("hfmoe_register_dense_layer", C.c_int, [C.c_int, C.POINTER(DenseWeights)]),
     ("hfmoe_register_lm_head", C.c_int, [C.c_void_p, C.c_void_p, C.c_int32]),
+    ("hfmoe_embedding_lookup", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
+    ("hfmoe_matvec_bf16", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+    ("hfmoe_softmax", C.c_int, [C.c_void_p, C.c_int]),
+    ("hfmoe_argmax", C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32)]),
+    ("hfmoe_embedding", C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
+    ("hfmoe_softmax_rows", C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
+    ("hfmoe_embedding_gather", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
+    ("hfmoe_matvec_bf16_dev", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    ("hfmoe_argmax_rows", C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_lm_head", C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("hfmoe_dense_mlp_forward", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_expert_cache_config", C.c_int, [C.c_int, C.c_int]),

@@ -163,6 +163,8 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
 void dense_workspace_free();
 // lm_head.hip
 void lm_head_release();
+hipError_t launch_row_argmax(const float* x, int T, int n, int* out, hipStream_t s);
+hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, int M, int K, float* y, hipStream_t s);
 // streamed.hip
 int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hipStream_t s,
                         const hfmoe_route_debug* dbg);

@@ -94,6 +94,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_gemv_kernel(const uint16_t* __res
             }
         }
     }
+    if (!part) return;  // plain matvec: no winner wanted
     __shared__ ArgMax wbest[kLmBlock / 64];
     if (lane == 0) wbest[wave] = {best, best_i};
     __syncthreads();
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(256) void argmax_merge_kernel(const ArgMax* __restr
     if (threadIdx.x == 0) *out = s[0].i == INT_MAX ? 0 : s[0].i;
 }
 
-// One block per token row of a [T, V] logits matrix.
+// One block per row of a [T, V] matrix: first index of the row's maximum.
 __global__ __launch_bounds__(256) void row_argmax_kernel(const float* __restrict__ logits, int V,
                                                          int* __restrict__ out) {
     __shared__ ArgMax s[256];
@@ -149,6 +150,10 @@ static hipError_t lm_gemv_inst(const uint16_t* W, const float* x, int V, int K, 
     return launch(lm_gemv_kernel<KCH, RF>, dim3(grid), dim3(kLmBlock), 0, s, W, x, V, K, logits, part);
 }
 
+hipError_t launch_row_argmax(const float* x, int T, int n, int* out, hipStream_t s) {
+    return launch(row_argmax_kernel, dim3(T), dim3(256), 0, s, x, n, out);
+}
+
 static hipError_t launch_lm_gemv(const uint16_t* W, const float* x, int V, int K, float* logits, ArgMax* part,
                                  int grid, hipStream_t s) {
     const int kch = (K + 511) / 512;
@@ -161,6 +166,11 @@ static hipError_t launch_lm_gemv(const uint16_t* W, const float* x, int V, int K
 
 // Two 4-wave blocks per CU (two rows of loads in flight per wavefront take
 // ~176 registers at hidden 6144; more rows or blocks measured no faster).
+// y[M] = W[M, K] . x[K] (K a multiple of 8, at most 8192), no argmax.
+hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, int M, int K, float* y, hipStream_t s) {
+    return launch_lm_gemv(W, x, M, K, y, nullptr, g.num_cus * 2, s);
+}
+
 static int lm_grid() { return env_int("HFMOE_LM_BLOCKS", g.num_cus * 2); }
 
 void lm_head_release() {

@@ -139,6 +139,24 @@ int hfmoe_register_lm_head(const uint16_t* lm_head_dev, const uint16_t* final_no
  * = first index of the largest logit (greedy sampling). */
 int hfmoe_lm_head(const float* h_dev, int32_t T, float* logits_dev, int32_t* token_dev, void* stream);
 
+/* ---- plugin helpers (cuda_backend.h:36-48): host buffers, synchronous ---- */
+int hfmoe_embedding_lookup(const uint16_t* emb_host, int token_id, float* out_host, int hidden); /* gpuEmbeddingLookup */
+int hfmoe_matvec_bf16(const uint16_t* w_host, const float* x_host, float* y_host, int M, int K);  /* gpuMatvecBf16 */
+int hfmoe_softmax(float* x_host, int n);                                                          /* gpuSoftmax */
+int hfmoe_argmax(const float* x_host, int n, int32_t* best);                                       /* gpuArgmax */
+/* Device forms, queued on `stream` (glm_cuda::embeddingGather / matvec /
+ * softmax / argmax, cuda_kernels.h:8-11).  hfmoe_embedding: out_dev[t, :] =
+ * emb_dev[ids_dev[t], :] as FP32, ids outside [0, vocab) give zeros;
+ * hfmoe_embedding_gather: one row, token_id < vocab is the caller's to check
+ * (as in the reference); softmax / argmax: each of T rows of n (argmax: the
+ * first largest element, an int32 per row). */
+int hfmoe_embedding(const uint16_t* emb_dev, int32_t vocab, int32_t hidden, const int32_t* ids_dev, int32_t T,
+                    float* out_dev, void* stream);
+int hfmoe_embedding_gather(const uint16_t* emb_dev, int token_id, float* out_dev, int hidden, void* stream);
+int hfmoe_matvec_bf16_dev(const uint16_t* w_dev, const float* x_dev, float* y_dev, int M, int K, void* stream);
+int hfmoe_softmax_rows(float* x_dev, int32_t T, int32_t n, void* stream);
+int hfmoe_argmax_rows(const float* x_dev, int32_t T, int32_t n, int32_t* best_dev, void* stream);
+
 /* ---- per-expert plugin surface (cuda_backend.h:64-90) ---- */
 int hfmoe_expert_cache_config(int capacity, int staging_depth); /* gpuExpertCacheConfig */
 void hfmoe_expert_cache_shutdown(void);                         /* gpuExpertCacheShutdown */

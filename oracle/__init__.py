@@ -81,6 +81,9 @@ def lib() -> C.CDLL:
                                    C.c_void_p]
         L.orc_expert_ffn.argtypes = [C.c_void_p] * 5 + [C.c_int, C.c_int, C.c_void_p]
         L.orc_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        L.orc_softmax.argtypes = [C.c_void_p, C.c_int]
+        L.orc_argmax.restype = C.c_int
+        L.orc_argmax.argtypes = [C.c_void_p, C.c_int]
         L.orc_moe_layer.restype = C.c_int
         L.orc_moe_layer.argtypes = [C.POINTER(MoeCfg), C.POINTER(MoeWeights), C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
@@ -125,6 +128,11 @@ def ref() -> C.CDLL | None:
         R.ref_rmsnorm.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float]
         R.ref_dense_mlp.restype = C.c_int
         R.ref_dense_mlp.argtypes = [C.c_char_p] + [C.c_void_p] * 3 + [C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        R.ref_embedding_lookup.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int]
+        R.ref_matvec_bf16.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        R.ref_softmax.argtypes = [C.c_void_p, C.c_int]
+        R.ref_argmax.restype = C.c_int
+        R.ref_argmax.argtypes = [C.c_void_p, C.c_int]
         R.ref_lm_head.restype = C.c_int
         R.ref_lm_head.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float,
                                   C.c_void_p, C.c_void_p, C.POINTER(C.c_int)]
@@ -229,6 +237,24 @@ def lm_head(W: np.ndarray, norm: np.ndarray | None, h: np.ndarray, vocab: int, e
     xn = rmsnorm(norm, h, eps)
     logits = gemv(np.ascontiguousarray(W, np.uint16).reshape(vocab, -1), xn)
     return logits, int(np.argmax(logits))
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    """The reference's softmax (cuda_backend.cpp:39-49): max, exp, one reciprocal."""
+    y = np.array(x, np.float32)
+    lib().orc_softmax(_p(y), len(y))
+    return y
+
+
+def argmax(x: np.ndarray) -> int:
+    """The reference's argmax (cuda_backend.cpp:51-57): first largest element."""
+    x = np.ascontiguousarray(x, np.float32)
+    return int(lib().orc_argmax(_p(x), len(x)))
+
+
+def embedding(emb: np.ndarray, token: int, hidden: int) -> np.ndarray:
+    """Row `token` of a BF16 [vocab, hidden] table widened to FP32 (cuda_backend.cpp:27-29)."""
+    return bf16_to_f32(np.ascontiguousarray(emb, np.uint16).reshape(-1, hidden)[token])
 
 
 # ------------------------------------------------------------ MoE layer ----

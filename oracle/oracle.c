@@ -173,6 +173,27 @@ void orc_expert_ffn(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd,
     orc_gemv_bf16_f32(Wd, m, y, hidden, inter, 1.0f, 0.0f);
 }
 
+/* cuda_backend.cpp:39-49 (and the CUDA-less gpuSoftmax, :577-588). */
+void orc_softmax(float* x, int n) {
+    float mx = x[0];
+    for (int i = 1; i < n; ++i) mx = fmaxf(mx, x[i]);
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        x[i] = expf(x[i] - mx);
+        sum += x[i];
+    }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < n; ++i) x[i] *= inv;
+}
+
+/* cuda_backend.cpp:51-57. */
+int orc_argmax(const float* x, int n) {
+    int best = 0;
+    for (int i = 1; i < n; ++i)
+        if (x[i] > x[best]) best = i;
+    return best;
+}
+
 /* glm_forward.cpp:185-197. */
 void orc_rmsnorm(const uint16_t* w, float* x, int n, float eps) {
     float sq = 0.0f;

@@ -82,6 +82,13 @@ void orc_expert_ffn(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd,
                     const float* x, float* y, int hidden, int inter,
                     float* scratch);
 
+/* ---- plugin helpers (cuda_backend.h:36-48; the reference's CPU forms,
+ * cuda_backend.cpp:27-57 and :564-594) ---- */
+/* x <- exp(x - max) * (1 / sum), serial order, libm expf. */
+void orc_softmax(float* x, int n);
+/* First index of the largest element (strictly greater replaces). */
+int orc_argmax(const float* x, int n);
+
 /* ---- RMSNorm (glm_forward.cpp:185-197) in place; w BF16 [n] or NULL ---- */
 void orc_rmsnorm(const uint16_t* w, float* x, int n, float eps);
 

@@ -13,6 +13,7 @@
 // template instantiation is not access-checked), with no change to any
 // reference header.
 #include "compute/cpu_kernels.h"
+#include "compute/cuda_backend.h"
 #include "compute/dtype_bf16.h"
 #include "compute/moe_router.h"
 #include "model/glm_forward.h"
@@ -327,5 +328,17 @@ int ref_lm_head(const char* path, const uint16_t* lm_head, const uint16_t* norm,
     ::unlink(path);
     return rc;
 }
+
+// The plugin helpers of src/compute/cuda_backend.h:36-48 as the reference
+// builds them without CUDA (cuda_backend.cpp:564-594): embedding row lookup,
+// row-major BF16 matvec, in-place softmax, argmax.
+void ref_embedding_lookup(const uint16_t* emb, int token, float* out, int hidden) {
+    glm::gpuEmbeddingLookup(reinterpret_cast<const glm::BFloat16*>(emb), token, out, hidden);
+}
+void ref_matvec_bf16(const uint16_t* W, const float* x, float* y, int M, int K) {
+    glm::gpuMatvecBf16(reinterpret_cast<const glm::BFloat16*>(W), x, y, M, K);
+}
+void ref_softmax(float* x, int n) { glm::gpuSoftmax(x, n); }
+int ref_argmax(const float* x, int n) { return glm::gpuArgmax(x, n); }
 
 }  // extern "C"

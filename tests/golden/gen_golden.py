@@ -6,7 +6,9 @@ output of the reference's functions -- gemv_bf16_f32 (cpu_kernels.cpp:43-94),
 sigmoid_f32 (moe_router.h:19-21), topKScores (moe_router.h:29-57),
 BFloat16::fromF32 (dtype_bf16.h:27-33), GLMForward::rmsNorm
 (glm_forward.cpp:185-197), GLMForward::moeLayer (glm_forward.cpp:509-661),
-GLMForward::denseMlp (:410-432) and GLMForward::lmHeadAndSample (:663-731) --
+GLMForward::denseMlp (:410-432), GLMForward::lmHeadAndSample (:663-731) and
+the plugin helpers gpuEmbeddingLookup / gpuMatvecBf16 / gpuSoftmax / gpuArgmax
+as built without CUDA (cuda_backend.cpp:564-594) --
 on inputs from the seeded generator, so the fixtures hold seeds, a few inputs
 and the reference's outputs, never reference source.
 
@@ -148,6 +150,41 @@ def main() -> None:
                    "top": top.tolist(), "top_bits": bits(lg[top]), "sample": sample.tolist(),
                    "sample_bits": bits(lg[sample])})
     g["lm_head"] = lm
+
+    # Plugin helpers (cuda_backend.h:36-48, the reference's CPU forms
+    # cuda_backend.cpp:564-594): embedding row, BF16 matvec, softmax, argmax.
+    helpers = {}
+    emb = O.fill_bf16(64 * 48, 9500, 1, 0.0, 1.0)
+    rows = []
+    for tok in (0, 5, 63):
+        out = np.zeros(48, np.float32)
+        R.ref_embedding_lookup(emb.ctypes.data, tok, out.ctypes.data, 48)
+        rows.append({"token": tok, "out": bits(out)})
+    helpers["embedding"] = {"vocab": 64, "hidden": 48, "seed": 9500, "rows": rows}
+    mv = []
+    for i, (M, K) in enumerate([(37, 300), (5, 6144)]):
+        W = O.fill_bf16(M * K, 9600 + i, 1, 0.0, 0.05)
+        x = O.fill_f32(K, 9600 + i, 2, 0.0, 1.0)
+        y = np.zeros(M, np.float32)
+        R.ref_matvec_bf16(W.ctypes.data, x.ctypes.data, y.ctypes.data, M, K)
+        mv.append({"M": M, "K": K, "seed": 9600 + i, "out": bits(y)})
+    helpers["matvec"] = mv
+    sm = []
+    for i, (n, sd) in enumerate([(1000, 3.0), (154880, 2.0), (7, 30.0)]):
+        x = O.fill_f32(n, 9700 + i, 1, 0.0, sd)
+        y = x.copy()
+        R.ref_softmax(y.ctypes.data, n)
+        sample = np.random.default_rng(9700 + i).choice(n, min(n, 64), replace=False)
+        sm.append({"n": n, "std": sd, "seed": 9700 + i, "sample": sample.tolist(), "sample_bits": bits(y[sample]),
+                   "sum64": float(np.sum(y, dtype=np.float64))})
+    helpers["softmax"] = sm
+    am = []
+    for i, n in enumerate([1000, 154880]):
+        x = O.fill_f32(n, 9800 + i, 1, 0.0, 1.0)
+        x[n // 3] = x[2 * n // 3] = float(np.max(x)) + 1.0  # an exact tie: the first wins
+        am.append({"n": n, "seed": 9800 + i, "best": int(R.ref_argmax(x.ctypes.data, n))})
+    helpers["argmax"] = am
+    g["helpers"] = helpers
 
     path = os.path.join(OUT, "reference_vectors.json")
     with open(path, "w") as f:

@@ -392,3 +392,39 @@ def test_lm_head_argmax_closed_form(oracle_lib):
     rows = np.stack([O.f32_to_bf16(s * xn) for s in (0.5, -1.0, 2.0, 1.0, 2.0)])
     logits, best = O.lm_head(rows, None, h, 5, 1e-5)
     assert best == 2 and logits[2] == logits[4]
+
+
+# --------------------------------------------------------- plugin helpers ----
+
+def test_helpers_match_reference(oracle_lib, golden):
+    O = oracle_lib
+    h = golden["helpers"]
+    e = h["embedding"]
+    emb = O.fill_bf16(e["vocab"] * e["hidden"], e["seed"], 1, 0.0, 1.0)
+    for r in e["rows"]:
+        got = O.embedding(emb, r["token"], e["hidden"])
+        assert np.array_equal(got.view(np.uint32), np.array(r["out"], np.uint32))
+    for c in h["matvec"]:
+        W = O.fill_bf16(c["M"] * c["K"], c["seed"], 1, 0.0, 0.05).reshape(c["M"], c["K"])
+        x = O.fill_f32(c["K"], c["seed"], 2, 0.0, 1.0)
+        assert np.array_equal(O.gemv(W, x).view(np.uint32), np.array(c["out"], np.uint32))
+    for c in h["softmax"]:
+        y = O.softmax(O.fill_f32(c["n"], c["seed"], 1, 0.0, c["std"]))
+        assert np.array_equal(y[c["sample"]].view(np.uint32), np.array(c["sample_bits"], np.uint32))
+        assert float(np.sum(y, dtype=np.float64)) == c["sum64"]
+    for c in h["argmax"]:
+        x = O.fill_f32(c["n"], c["seed"], 1, 0.0, 1.0)
+        x[c["n"] // 3] = x[2 * c["n"] // 3] = float(np.max(x)) + 1.0
+        assert O.argmax(x) == c["best"] == c["n"] // 3
+
+
+def test_softmax_closed_forms(oracle_lib):
+    # Equal inputs give 1/n exactly (n a power of two); a shift by a constant
+    # changes nothing once the maximum is subtracted; one dominant entry -> 1.
+    O = oracle_lib
+    assert np.all(O.softmax(np.full(64, 3.25, np.float32)) == np.float32(1 / 64))
+    x = O.fill_f32(100, 4, 1, 0.0, 1.0)
+    xs = (x + np.float32(16.0)).astype(np.float32)
+    assert np.allclose(O.softmax(x), O.softmax(xs), rtol=1e-5, atol=1e-8)
+    y = O.softmax(np.array([0.0, 200.0, 0.0], np.float32))
+    assert y[1] == 1.0 and y[0] == y[2] == 0.0  # exp(-200) underflows in FP32
