@@ -83,7 +83,7 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
         return HFMOE_OK;
     }
     GroupedWorkspace& gw = g.gws;
-    const int TR = T >= 192 ? 256 : kGemmTileRows;
+    const int TR = T >= 192 ? kDenseTileRows : kGemmTileRows;
     const int I = L.dense_inter;
     prof_begin(p, "split_x", s);
     HF_CHECK_LAUNCH(launch_split_bf16(x, gw.xh, gw.xl, (size_t)T * c.d, gw.lo_flag, s), "split x");
@@ -91,8 +91,8 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     gu.K = c.d;
     gu.N = I;
     gu.tile_rows = TR;
-    gu.tile_cols = TR;
-    gu.n_tiles = (I + TR / 2 - 1) / (TR / 2);
+    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU);
+    gu.n_tiles = gemm_n_tiles(EPI_SWIGLU, I, gu.tile_cols);
     gu.m_tiles = (T + TR - 1) / TR;
     gu.rows_total = T;
     gu.a_hi = gw.xh;
@@ -110,8 +110,8 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     dn.K = I;
     dn.N = c.d;
     dn.tile_rows = TR;
-    dn.tile_cols = TR;
-    dn.n_tiles = (c.d + TR - 1) / TR;
+    dn.tile_cols = gemm_tile_cols(TR, EPI_PARTIAL);
+    dn.n_tiles = gemm_n_tiles(EPI_PARTIAL, c.d, dn.tile_cols);
     dn.m_tiles = (T + TR - 1) / TR;
     dn.rows_total = T;
     dn.a_hi = w.hh;

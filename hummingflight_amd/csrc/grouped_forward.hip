@@ -35,17 +35,17 @@ static int router_ksplit(int T) {
 }
 
 // Persistent grid: two 4-wave workgroups per CU (128-row tiles) or one
-// workgroup per CU (256-row tiles).
+// workgroup per CU (larger tiles).
 int gemm_blocks(int tile_rows) {
-    return env_int("HFMOE_GEMM_BLOCKS", tile_rows == 256 ? g.num_cus : g.num_cus * 2);
+    return env_int("HFMOE_GEMM_BLOCKS", tile_rows == kGemmTileRows ? g.num_cus * 2 : g.num_cus);
 }
 
-// 256 x 256 tiles once experts average 96+ rows (prefill): an expert's rows
+// Prefill tiles (192 x 384) once experts average 96+ rows: an expert's rows
 // then fit one tile, its weights stream through the memory system once, and
-// each activation row is requested once per 256 weight rows.
+// each activation row is requested once per 384 weight rows.
 static int expert_tile_rows(int T) {
     const Cfg& c = g.cfg;
-    return (size_t)T * c.k >= (size_t)96 * c.E ? 256 : kGemmTileRows;
+    return (size_t)T * c.k >= (size_t)96 * c.E ? kPrefillTileRows : kGemmTileRows;
 }
 
 void grouped_workspace_free() {
@@ -154,8 +154,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.K = c.d;
     gu.N = c.I;
     gu.tile_rows = TR;
-    gu.tile_cols = TR;
-    gu.n_tiles = (c.I + TR / 2 - 1) / (TR / 2);
+    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU);
+    gu.n_tiles = gemm_n_tiles(EPI_SWIGLU, c.I, gu.tile_cols);
     gu.tile_group = w.tile_expert;
     gu.tile_row0 = w.tile_row0;
     gu.ntiles_dev = w.ntiles;
@@ -180,8 +180,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.K = c.I;
     dn.N = c.d;
     dn.tile_rows = TR;
-    dn.tile_cols = TR;
-    dn.n_tiles = (c.d + TR - 1) / TR;
+    dn.tile_cols = gemm_tile_cols(TR, EPI_SCATTER);
+    dn.n_tiles = gemm_n_tiles(EPI_SCATTER, c.d, dn.tile_cols);
     dn.tile_group = w.tile_expert;
     dn.tile_row0 = w.tile_row0;
     dn.ntiles_dev = w.ntiles;

@@ -14,22 +14,26 @@
 //
 // The MoE GEMMs stream expert weights (B) far more than they compute: at
 // T = 4096 each expert sees ~128 rows, 128 FLOP per weight byte, below the
-// MI355X ridge (~312), and at T = 64 a few rows.  So the kernel is built to
-// keep B streaming and to spend MFMA cycles only on rows that exist:
-//   * tile 128 or 256 (M) x 128 (N) x 64 (K), 4 or 8 wavefronts; wavefront w
-//     owns tile rows [32w, 32w + 32) across all 128 columns and skips the
-//     MFMAs of 16-row blocks past the group's last row, so a 3-row expert
-//     costs one 16-row block of work, not 128;
-//   * B goes straight from global memory into an LDS ring by DMA
-//     (global_load_lds_dwordx4) with no register staging, and A fragments
+// MI355X ridge (~312), and at T = 64 a few rows.  So the kernels are built to
+// keep B streaming and to spend MFMA cycles only on rows that exist.  Two
+// tile shapes:
+//   * 128 (M) x 128 (N) x 64 (K), 4 wavefronts (batched decode, router):
+//     wavefront w owns tile rows [32w, 32w + 32) across all 128 columns and
+//     skips the MFMAs of 16-row blocks past the group's last row, so a 3-row
+//     expert costs one 16-row block of work, not 128.  B goes from global
+//     memory into an LDS ring by DMA (global_load_lds_dwordx4), A fragments
 //     straight into registers (L2-resident activations, row-gathered through
-//     a_rowmap); both are fetched 2-4 K stages ahead of the one multiplied;
-//   * persistent workgroups walk per-XCD item lists, n fastest, so an M
-//     tile's activations are reused within that XCD's L2 (item_range).
+//     a_rowmap), both 2-4 K stages ahead of the one multiplied;
+//   * 192 (M) x 256 or 384 (N) x 64 (K), 8 wavefronts (prefill): both
+//     operands by DMA into LDS, wavefronts split 2 (row-block parity) x 4
+//     (column groups) -- gemm_item_split below.
+// Persistent workgroups walk per-XCD item lists, n fastest, so an M tile's
+// activations are reused within that XCD's L2 (item_range).
 //
 // Epilogues:
-//   PARTIAL  split-K partial sums (router logits; reduced in fixed order later)
-//   SWIGLU   B rows = 64 gate rows then the 64 matching up rows; writes
+//   PARTIAL  split-K partial sums (router logits; reduced in fixed order
+//            later), or plain FP32 rows with ksplit = 1 (dense down)
+//   SWIGLU   B rows = gate rows then as many matching up rows; writes
 //            h = silu(g) * u as BF16 hi/lo (glm_forward.cpp:444-446)
 //   SCATTER  y for one (token, rank) pair per row, stored at row scatter_rows[r]
 #include "hf_api_internal.h"
@@ -70,9 +74,11 @@ constexpr size_t kRingBytes = sizeof(BStage) * (kDepthHi + 1);
 // Weight DMA with the non-temporal hint: each weight tile is read by at most
 // the few M tiles of one expert, close together in time, while the activation
 // rows are re-read by every N tile of their M tile and must stay in L2.
+// (POLICY 0: the activations' DMA, which should stay in L2.)
+template <int POLICY = kDmaPolicy>
 __device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* l) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)l, 16, 0, kDmaPolicy);
+                                     (__attribute__((address_space(3))) void*)l, 16, 0, POLICY);
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
@@ -95,11 +101,11 @@ __device__ __forceinline__ void lds_barrier() {
 // hardware deals workgroups to the 8 XCDs round-robin, so blockIdx.x % 8 is
 // the XCD, and each XCD takes a contiguous range of items (an M tile's N
 // tiles, which share its activation rows, run side by side in one L2).
-// DEAL_M (256-row prefill tiles, at least one M tile per XCD): whole M tiles
-// are dealt to the XCDs round-robin instead, which keeps the first property
-// and spreads runs of heavy tiles -- the shared expert's full 256-row tiles
-// sit together at the end of the list, with twice the MFMA work of a routed
-// expert's ~128 rows -- over all XCDs rather than the last one.
+// DEAL_M (prefill tiles, at least one M tile per XCD): whole M tiles are
+// dealt to the XCDs round-robin instead, which keeps the first property and
+// spreads runs of heavy tiles -- the shared expert's full 192-row tiles sit
+// together at the end of the list, with half as much again the MFMA work of a
+// routed expert's ~128 rows -- over all XCDs rather than the last one.
 struct ItemRange {
     int begin, end, stride;  // local item indices begin, begin + stride, ... < end
     int xcd, nxcd, per_m;    // per_m = n_tiles * ksplit items per M tile
@@ -374,9 +380,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
 // also leaves it more registers).
 enum { kLoNone = 0, kLoByFlag = 1, kLoAlways = 2 };
 
-// WAVES = 4: 128-row tiles, two workgroups per CU; WAVES = 8: 256-row tiles
-// (one expert's rows in one tile at prefill sizes, so each weight tile
-// crosses the memory system once), one workgroup per CU.
+// WAVES = 4: 128-row tiles, two workgroups per CU.
 template <int EPI, int LOM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) BStage ring[];  // kRingBytes
@@ -400,39 +404,100 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 }
 
 // ---------------------------------------------------------------------------
-// Wide tiles for prefill: 256 (M) x 256 (N) x 64 (K), eight wavefronts, one
-// workgroup per CU.  Wavefront w owns tile rows [32w, 32w + 32) across all 256
-// columns, so each A fragment serves twice the columns of the 128-column tile
-// and the activation requests per FLOP halve -- at prefill sizes the CUs'
-// request bandwidth to L2, not HBM, bounds these GEMMs.  Same pipeline as
-// gemm_item: B by DMA into an LDS ring, A into registers, both D stages
-// ahead, explicit counter waits.
-constexpr int kWideRows = 256, kWideCols = 256;
-typedef uint16_t WStage[kWideCols * GBK];  // 32 KB: 256 weight rows x 64 k
-constexpr int kWideDepthHi = 2, kWideDepthLo = 1;
-constexpr size_t kWideRingBytes = sizeof(WStage) * (kWideDepthHi + 1);
+// Split tiles for prefill: ROWS (M) x 64*CB (N) x 64 (K), eight wavefronts,
+// one workgroup per CU.  Both operands go by DMA into LDS rings in whole
+// 128-byte lines: activations (A, up to ROWS rows of the group, L2-resident)
+// and weights (B, 64*CB weight rows streamed from HBM with the non-temporal
+// hint).  Wavefront w takes column group w & 3 (16*CB output columns; SWIGLU:
+// 8*CB h columns from as many gate and up rows) and the row blocks of parity
+// w >> 2, so each wavefront reads a quarter of B and half of A from LDS, and a
+// group of n row blocks gives every wavefront ceil(n / 2) or floor(n / 2) of
+// them: the MFMA work stays even across the SIMDs for any row count.
+//
+// ROWS = 192 for the MoE GEMMs: a routed expert's ~128 rows at T = 4096 fit
+// one tile with room to spare (an expert with more takes several M tiles and
+// re-reads its weights).  ROWS = 256 for one-group GEMMs (dense layers, LM
+// head), whose weights are re-read once per M tile.
+//
+// What bounds these GEMMs is the number of memory requests in flight per CU
+// (each CU's vector L1 holds a limited number of outstanding 128-byte line
+// requests, and at ~640 cycles of average latency that caps a CU near
+// 15 B/cycle), so the tile is as wide as the accumulators allow: every N tile
+// re-reads its M tile's activations, and 384 columns (CB = 6, 144 registers
+// of accumulators per lane) cut those re-reads by a third against 256.
+//
+// The lo half of A runs as its own sub-step against the same B stage, so an
+// A stage is always one half (ROWS x 64 BF16): sub-step j = HALVES * s + half
+// multiplies A half `half` of K stage s.  A runs DA sub-steps and B DB K
+// stages ahead; the rings hold RA = DA + 1 A stages and RB = DB + 1 B stages.
+// Column blocks per wavefront: 256-row tiles 4; 192-row tiles 6 for the down
+// projection (384 weight rows) and 4 for gate/up, which leaves LDS for weights
+// two stages ahead.
+template <int EPI, int ROWS>
+constexpr int split_cb() { return ROWS == 256 || EPI == EPI_SWIGLU ? 4 : 6; }
+// Stages ahead (A in sub-steps, B in K stages) and the LDS they take.
+constexpr int split_da(int ROWS, int CB, int H) { return ROWS == 256 && H == 2 ? 2 : 1; }
+constexpr int split_db(int ROWS, int CB, int H) { return CB == 6 || (ROWS == 256 && H == 2) ? 1 : 2; }
+constexpr size_t split_lds(int ROWS, int CB, int H) {
+    return 2 * ((size_t)(split_da(ROWS, CB, H) + 1) * ROWS * GBK + (size_t)(split_db(ROWS, CB, H) + 1) * 64 * CB * GBK);
+}
+constexpr size_t split_lds_max(int ROWS, int CB) {
+    return split_lds(ROWS, CB, 1) > split_lds(ROWS, CB, 2) ? split_lds(ROWS, CB, 1) : split_lds(ROWS, CB, 2);
+}
+static_assert(split_lds_max(192, 4) <= 160 * 1024 && split_lds_max(192, 6) <= 160 * 1024 &&
+                  split_lds_max(256, 4) <= 160 * 1024,
+              "LDS");
 
-template <int EPI, bool USE_LO>
-__device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WStage* ring, int t, int wave) {
-    constexpr int BJ = 4;  // 1 KB weight DMAs per wave per stage (32 per stage)
-    constexpr int cols_per_tile = EPI == EPI_SWIGLU ? kWideCols / 2 : kWideCols;
-    constexpr int NA = USE_LO ? 8 : 4;  // A loads per wave per stage
-    constexpr int D = USE_LO ? kWideDepthLo : kWideDepthHi;
-    constexpr int RING = D + 1;
+// DMA instructions a wavefront may leave outstanding at sub-step j (half =
+// j % H) once A(j) and B(j / H) have landed, in the steady issue pattern
+// "sub-step q issues A(q + DA), then B(q / H + DB) when q % H == 0" (loads
+// complete in issue order): those issued after the later of the two.
+constexpr int split_after(int H, int DA, int DB, int half, int NAD, int NBD) {
+    const int s0 = 16;  // any stage past the prologue
+    const int j = s0 * H + half;
+    const int pa = j - DA;         // A(j): first op of sub-step pa
+    const int pb = H * (s0 - DB);  // B(s0): second op of sub-step pb
+    int n = 0, p;
+    if (pa > pb) {
+        p = pa;
+        if (p % H == 0) n += NBD;  // that sub-step's B follows A(j)
+    } else {
+        p = pb;
+    }
+    for (int q = p + 1; q < j; ++q) n += NAD + (q % H == 0 ? NBD : 0);
+    return n;
+}
+
+template <int EPI, int ROWS, int HALVES>
+__device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave) {
+    constexpr int CB = split_cb<EPI, ROWS>();
+    constexpr int RBW = ROWS / 32;                 // row blocks per wavefront
+    constexpr int AST = ROWS * GBK;                // elements per A stage
+    constexpr int NAD = ROWS / 64, NBD = CB;       // 1 KB DMAs per wave per stage: activations, weights
+    constexpr int DA = split_da(ROWS, CB, HALVES), DB = split_db(ROWS, CB, HALVES);
+    constexpr int RA = DA + 1, RB = DB + 1;
+    constexpr int cols_per_tile = EPI == EPI_SWIGLU ? 32 * CB : 64 * CB;
+    uint16_t* aring = lds;
+    uint16_t* bring = lds + RA * AST;
     const int lane = t & 63;
     const int fr = lane & 15;
     const int fq = lane >> 4;
+    const int cg = wave & 3;
+    const int par = wave >> 2;
     const int Kc = a.K / a.ksplit;
     const int nk = Kc / GBK;
+    const int nj = nk * HALVES;
 
     const int ks = item % a.ksplit;
     const int rest = item / a.ksplit;
     const int nt = rest % a.n_tiles;
     const int mt = rest / a.n_tiles;
     const int g = a.tile_group ? a.tile_group[mt] : 0;
-    const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * kWideRows;
+    const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * ROWS;
     const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
-    const int rows = min(kWideRows, row_end - row0);
+    const int rows = min(ROWS, row_end - row0);
+    const int nrb = (rows + 15) >> 4;
+    const int nmine = (nrb - par + 1) >> 1;  // row blocks 2j + par, j < nmine
     const int n0 = nt * cols_per_tile;
     const uint16_t* b0;
     const uint16_t* b1 = nullptr;
@@ -444,139 +509,119 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, WSta
         b1 = a.b_fixed1;
     }
     const int kbase = ks * Kc;
-    const int wrows = min(max(rows - 32 * wave, 0), 32);
-    const int nrb = (wrows + 15) >> 4;
 
-    // A rows of row blocks 0 and 1 (the lo half sits at a fixed offset from
-    // the hi half, so one pointer per row block serves both).
-    const uint16_t* ap[2];
-    const ptrdiff_t lo_off = USE_LO ? a.a_lo - a.a_hi : 0;
+    // DMA slot i (16 bytes) of a stage holds chunk (i & 7) ^ (r & 7) of stage
+    // row r = i >> 3.  Activation rows past the tile's end re-read its last
+    // row.  Weight rows: SWIGLU rows [0, 32 CB) are gate rows n0.., the next
+    // 32 CB the matching up rows; a wavefront's 8 CB slot rows lie in one half.
+    uint32_t aoff[NAD], boff[NBD];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const int lr = min(32 * wave + 16 * rb + fr, rows - 1);
-        const int gr = row0 + lr;
-        const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
-        ap[rb] = a.a_hi + src * a.K + kbase + fq * 8;
-    }
-    // Ring slot i (16 bytes) of a stage holds chunk (i & 7) ^ (row & 7) of tile
-    // row i >> 3; SWIGLU rows 0-127 are gate rows n0.., 128-255 the up rows.
-    // A wavefront's 32 slot rows lie in one half, so one base pointer plus
-    // 32-bit element offsets addresses them.
-    const uint16_t* bbase = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
-    uint32_t boff[BJ];
-#pragma unroll
-    for (int j = 0; j < BJ; ++j) {
-        const int i = (wave * BJ + j) * 64 + lane;
+    for (int j = 0; j < NAD; ++j) {
+        const int i = (wave * NAD + j) * 64 + lane;
         const int r = i >> 3;
         const int c = (i & 7) ^ (r & 7);
-        int n = EPI == EPI_SWIGLU ? n0 + (r & 127) : n0 + r;
+        const int gr = row0 + min(r, rows - 1);
+        const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
+        aoff[j] = (uint32_t)(src * a.K + kbase + c * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < NBD; ++j) {
+        const int i = (wave * NBD + j) * 64 + lane;
+        const int r = i >> 3;
+        const int c = (i & 7) ^ (r & 7);
+        int n = EPI == EPI_SWIGLU ? n0 + r % (32 * CB) : n0 + r;
         n = min(n, a.N - 1);
         boff[j] = (uint32_t)((size_t)n * a.b_ld + kbase + c * 8);
     }
+    const uint16_t* bbase = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
+    const ptrdiff_t lo_off = HALVES == 2 ? a.a_lo - a.a_hi : 0;
 
-    f32x4_t acc[2][16];
+    f32x4_t acc[RBW][CB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int j = 0; j < RBW; ++j)
 #pragma unroll
-        for (int cb = 0; cb < 16; ++cb) acc[rb][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int cb = 0; cb < CB; ++cb) acc[j][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto issue_b = [&](int s) {
-        uint16_t* dst = ring[s % RING] + wave * BJ * 512;
-        s = min(s, nk - 1);
+    // Sub-step / stage indices outside [0, nj) / [0, nk) (prologue and tail)
+    // load the nearest valid one into the slot of the index itself: a slot
+    // that nothing reads before its own stage lands there, in issue order.
+    auto issue_a = [&](int j) {  // A half of sub-step j
+        uint16_t* dst = aring + ((j % RA + RA) % RA) * AST + wave * NAD * 512;
+        j = min(max(j, 0), nj - 1);
+        const uint16_t* src = a.a_hi + (j % HALVES ? lo_off : 0) + (j / HALVES) * GBK;
 #pragma unroll
-        for (int j = 0; j < BJ; ++j) dma16(bbase + boff[j] + s * GBK, dst + j * 512);
+        for (int i = 0; i < NAD; ++i) dma16<0>(src + aoff[i], dst + i * 512);
     };
-    typedef u32x4 AFrag[2][2][2];  // [hi/lo][row block][k half]
-    auto load_a = [&](AFrag& f, int s) {
-        s = min(s, nk - 1);
+    auto issue_b = [&](int s) {  // B of K stage s
+        uint16_t* dst = bring + ((s % RB + RB) % RB) * (64 * CB * GBK) + wave * NBD * 512;
+        s = min(max(s, 0), nk - 1);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                f[0][rb][kh] = ld_global(ap[rb] + s * GBK + kh * 32);
-                if (USE_LO) f[1][rb][kh] = ld_global(ap[rb] + lo_off + s * GBK + kh * 32);
-            }
+        for (int i = 0; i < NBD; ++i) dma16(bbase + boff[i] + s * GBK, dst + i * 512);
     };
-    // Eight groups of four column blocks (k half kh = g >> 2, quarter g & 3);
-    // group g+1's B fragments are read while group g's MFMAs run (hi-only
-    // path; with the lo half the registers go to the lo A fragments instead).
-    constexpr int NB = USE_LO ? 1 : 2;
-    auto compute = [&](const uint16_t* bt, const AFrag& f) {
-        if (nrb == 0) return;
-        bf16x8_t bf[NB][4];
-        auto read_group = [&](int gi, bf16x8_t(&dst)[4]) {
-            const int kh = gi >> 2, cq = gi & 3;
+    // B stage row of this wavefront's column block cb.  The weights are the
+    // MFMA's first operand, so lane (fr, fq) ends with output columns
+    // 4 fq .. 4 fq + 3 of the block for row fr of the row block.
+    auto brow = [&](int cb) {
+        return EPI == EPI_SWIGLU ? (cb < CB / 2 ? 8 * CB * cg + 16 * cb : 32 * CB + 8 * CB * cg + 16 * (cb - CB / 2)) + fr
+                                 : 16 * CB * cg + 16 * cb + fr;
+    };
+    auto compute = [&](const uint16_t* at, const uint16_t* bt) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = 16 * (4 * cq + j) + fr;
+        for (int kh = 0; kh < 2; ++kh) {
+            bf16x8_t w[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int r = brow(cb);
                 const int c = (kh * 4 + fq) ^ (r & 7);
-                dst[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
+                w[cb] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
             }
-        };
-        if (NB == 2) read_group(0, bf[0]);
 #pragma unroll
-        for (int gi = 0; gi < 8; ++gi) {
-            if (NB == 1)
-                read_group(gi, bf[0]);
-            else if (gi + 1 < 8)
-                read_group(gi + 1, bf[(gi + 1) % NB]);
-            const int kh = gi >> 2, cq = gi & 3;
-            const bf16x8_t(&b)[4] = bf[gi % NB];
+            for (int j = 0; j < RBW; ++j) {
+                if (j < nmine) {  // a guard, not a break: acc must stay in registers
+                    const int r = 16 * (2 * j + par) + fr;
+                    const int c = (kh * 4 + fq) ^ (r & 7);
+                    const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4*>(at + r * GBK + c * 8));
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                if (rb == 1 && nrb < 2) break;
-                const bf16x8_t af = as_bf16x8(f[0][rb][kh]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[rb][4 * cq + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], af, acc[rb][4 * cq + j], 0, 0, 0);
-                if (USE_LO) {
-                    const bf16x8_t alf = as_bf16x8(f[1][rb][kh]);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[rb][4 * cq + j] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], alf, acc[rb][4 * cq + j], 0, 0, 0);
+                    for (int cb = 0; cb < CB; ++cb)
+                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[cb], av, acc[j][cb], 0, 0, 0);
                 }
             }
         }
     };
-    auto step = [&](int s, const AFrag& cur, AFrag& ahead, auto tail) {
-        if constexpr (decltype(tail)::value)
-            wait_vmcnt<0>();
-        else
-            wait_vmcnt<(D - 1) * (NA + BJ)>();
+    auto substep = [&](int s, auto half_c) {
+        constexpr int half = decltype(half_c)::value;
+        const int j = s * HALVES + half;
+        wait_vmcnt<split_after(HALVES, DA, DB, half, NAD, NBD)>();
         lds_barrier();
-        load_a(ahead, s + D);
-        issue_b(s + D);
-        compute(ring[s % RING], cur);
+        issue_a(j + DA);
+        if (half == 0) issue_b(s + DB);
+        compute(aring + (j % RA) * AST, bring + (s % RB) * (64 * CB * GBK));
     };
-
-    AFrag A[RING];
+    // Prologue: the sub-steps before 0 of the steady pattern (ops with an
+    // index below 0 load stage 0 into the slot of that index), so the counts
+    // split_after assumes hold from sub-step 0 on.
+    constexpr int Q = DA > HALVES * DB ? DA : HALVES * DB;
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-        load_a(A[j], j);
-        issue_b(j);
+    for (int q = -Q; q < 0; ++q) {
+        issue_a(q + DA);
+        if ((q % HALVES) == 0) issue_b(q / HALVES + DB);
     }
-    int s = 0;
-    for (; s + RING <= nk; s += RING) {
-#pragma unroll
-        for (int u = 0; u < RING; ++u) step(s + u, A[u], A[(u + D) % RING], std::false_type{});
+    for (int s = 0; s < nk; ++s) {
+        substep(s, std::integral_constant<int, 0>{});
+        if constexpr (HALVES == 2) substep(s, std::integral_constant<int, 1>{});
     }
-#pragma unroll
-    for (int u = 0; u < RING - 1; ++u)
-        if (s + u < nk) step(s + u, A[u], A[(u + D) % RING], std::true_type{});
 
-    // Epilogue: as in gemm_item, 4 adjacent output columns per store.
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        if (rb >= nrb) break;
-        const int rl = 32 * wave + 16 * rb + fr;
-        if (rl < rows) store_tile_row<EPI, 16>(a, acc[rb], row0 + rl, n0 + 4 * fq, ks);
+    for (int j = 0; j < RBW; ++j) {
+        const int rl = 16 * (2 * j + par) + fr;
+        const int col0 = EPI == EPI_SWIGLU ? n0 + 8 * CB * cg + 4 * fq : n0 + 16 * CB * cg + 4 * fq;
+        if (j < nmine && rl < rows) store_tile_row<EPI, CB>(a, acc[j], row0 + rl, col0, ks);
     }
 }
 
-template <int EPI, int LOM>
-__global__ __launch_bounds__(512, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
-    extern __shared__ __attribute__((aligned(16))) WStage wring[];  // kWideRingBytes
+template <int EPI, int LOM, int ROWS>
+__global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t slds[];  // split_lds_max(ROWS, CB) bytes
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
@@ -584,12 +629,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
     for (int li = r.begin; li < r.end; li += r.stride) {
         const int item = r.item(li);
-        if constexpr (LOM == kLoAlways)
-            gemm_item_wide<EPI, true>(a, item, wring, t, wave);
-        else if (LOM == kLoByFlag && use_lo)
-            gemm_item_wide<EPI, LOM == kLoByFlag>(a, item, wring, t, wave);
+        if (LOM != kLoNone && use_lo)
+            gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
         else
-            gemm_item_wide<EPI, false>(a, item, wring, t, wave);
+            gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave);
         __syncthreads();
     }
 }
@@ -666,24 +709,24 @@ static hipError_t launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
     return launch(grouped_gemm_kernel<EPI, LOM, WAVES>, dim3(blocks), dim3(64 * WAVES), (uint32_t)kRingBytes, s, a);
 }
 
-template <int EPI, int LOM>
-static hipError_t launch_gemm_wide(const GemmArgs& a, int blocks, hipStream_t s) {
+template <int EPI, int LOM, int ROWS>
+static hipError_t launch_gemm_split(const GemmArgs& a, int blocks, hipStream_t s) {
+    constexpr size_t lds = split_lds_max(ROWS, split_cb<EPI, ROWS>());
     static bool raised = false;
     if (!raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel<EPI, LOM>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideRingBytes);
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_split_kernel<EPI, LOM, ROWS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         raised = true;
     }
-    return launch(grouped_gemm_wide_kernel<EPI, LOM>, dim3(blocks), dim3(512), (uint32_t)kWideRingBytes, s, a);
+    return launch(grouped_gemm_split_kernel<EPI, LOM, ROWS>, dim3(blocks), dim3(512), (uint32_t)lds, s, a);
 }
 
 template <int EPI, int LOM>
 static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
-    if (a.tile_rows == 256 && a.tile_cols == 256) return launch_gemm_wide<EPI, LOM>(a, blocks, s);
-    if (a.tile_cols != 128) return hipErrorInvalidValue;
-    if (a.tile_rows == 256) return launch_gemm<EPI, LOM, 8>(a, blocks, s);
-    if (a.tile_rows == 128) return launch_gemm<EPI, LOM, 4>(a, blocks, s);
+    if (a.tile_rows == 192 && a.tile_cols == 64 * split_cb<EPI, 192>()) return launch_gemm_split<EPI, LOM, 192>(a, blocks, s);
+    if (a.tile_rows == 256 && a.tile_cols == 64 * split_cb<EPI, 256>()) return launch_gemm_split<EPI, LOM, 256>(a, blocks, s);
+    if (a.tile_rows == kGemmTileRows && a.tile_cols == GBN) return launch_gemm<EPI, LOM, 4>(a, blocks, s);
     return hipErrorInvalidValue;
 }
 

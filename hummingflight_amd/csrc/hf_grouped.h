@@ -5,18 +5,34 @@
 
 namespace hf {
 
-constexpr int kGemmTileRows = 128;  // M rows per grouped-GEMM tile (256 at prefill sizes)
+constexpr int kGemmTileRows = 128;  // M rows per grouped-GEMM tile (kPrefillTileRows at prefill sizes)
+// Prefill tiles: 192 rows (a routed expert's rows at T = 4096 in one tile);
+// one-group GEMMs (dense layers, LM head) with T >= 192: 256 rows.
+constexpr int kPrefillTileRows = 192, kDenseTileRows = 256;
 constexpr int kGemmTileK = 64;      // K per pipeline stage (K % (64 * ksplit) == 0)
 
 enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
+
+// Weight rows per tile for M tiles of tile_rows rows (MoE prefill: 256 for
+// gate/up, i.e. 128 gate + 128 up rows, and 384 otherwise; one-group GEMMs
+// with 256-row tiles: 256), and the N tiles that cover N output columns (a
+// SWIGLU tile's weight rows are half gate, half up).
+inline int gemm_tile_cols(int tile_rows, int epi) {
+    if (tile_rows == kPrefillTileRows) return epi == EPI_SWIGLU ? 256 : 384;
+    return tile_rows == kDenseTileRows ? 256 : 128;
+}
+inline int gemm_n_tiles(int epi, int N, int tile_cols) {
+    const int cols = epi == EPI_SWIGLU ? tile_cols / 2 : tile_cols;
+    return (N + cols - 1) / cols;
+}
 
 // Arguments of one grouped GEMM launch (see grouped_gemm.hip).
 struct GemmArgs {
     int K;                      // reduction length (multiple of 64 * ksplit)
     int N;                      // output columns (SWIGLU: intermediate rows per matrix)
     int n_tiles;                // ceil(N / output columns per tile); SWIGLU: tile_cols / 2 per tile
-    int tile_rows;              // M rows per tile: 128 or 256
-    int tile_cols;              // B rows (weight rows) per tile: 128, or 256 with 256-row tiles
+    int tile_rows;              // M rows per tile: kGemmTileRows (or 256) or kPrefillTileRows
+    int tile_cols;              // B rows (weight rows) per tile: gemm_tile_cols(tile_rows)
     // M tiling: tile i covers rows [tile_row0[i], min(+tile_rows, group_end[tile_group[i]]))
     const int* tile_group;      // null: one group, rows [0, rows_total) in tile_rows-row tiles
     const int* tile_row0;

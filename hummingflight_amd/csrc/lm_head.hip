@@ -211,13 +211,13 @@ static int lm_head_forward(const float* h, int T, float* logits, int* token, hip
     GroupedWorkspace& gw = g.gws;
     prof_begin(p, "split_x", s);
     HF_CHECK_LAUNCH(launch_split_bf16(xn, gw.xh, gw.xl, (size_t)T * c.d, gw.lo_flag, s), "split x");
-    const int TR = T >= 192 ? 256 : kGemmTileRows;
+    const int TR = T >= 192 ? kDenseTileRows : kGemmTileRows;
     GemmArgs a{};
     a.K = c.d;
     a.N = L.vocab;
     a.tile_rows = TR;
-    a.tile_cols = TR == 256 ? 256 : 128;
-    a.n_tiles = (L.vocab + a.tile_cols - 1) / a.tile_cols;
+    a.tile_cols = gemm_tile_cols(TR, EPI_PARTIAL);
+    a.n_tiles = gemm_n_tiles(EPI_PARTIAL, L.vocab, a.tile_cols);
     a.m_tiles = (T + TR - 1) / TR;
     a.rows_total = T;
     a.a_hi = gw.xh;

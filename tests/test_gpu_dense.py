@@ -3,7 +3,7 @@
 The oracle's dense_mlp is pinned bit-exact to the reference's own denseMlp
 (tests/test_oracle.py).  Here the library's decode path (T = 1: the expert
 GEMVs over inter / slice slices) and multi-token path (one-group grouped GEMM,
-128- and 256-row tiles) must agree with it within 1e-2 relative + 2e-3
+128- and 192-row tiles) must agree with it within 1e-2 relative + 2e-3
 absolute, at a small shape and at GLM-5.2's (hidden 6144, intermediate 12288);
 the RMSNorm + residual block and a dense layer loaded from a checkpoint too.
 """
@@ -72,7 +72,7 @@ def test_dense_small_decode_and_batches(hf):
     x1 = rng.standard_normal((1, H)).astype(np.float32)
     y1 = L.forward(x1)
     assert_close(y1[0], L.ref(x1[0]), "T=1")
-    for T in (5, 300):  # 128-row and 256-row tiles
+    for T in (5, 300):  # 128-row and 192-row tiles (two M tiles)
         x = rng.standard_normal((T, H)).astype(np.float32)
         y = L.forward(x)
         for t in sorted({0, T // 2, T - 1}):

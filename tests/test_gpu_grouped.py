@@ -57,8 +57,9 @@ def test_grouped_small(hf, T):
     r.free()
 
 
-def test_grouped_small_256_row_tiles(hf):
-    # 96+ rows per expert on average: the grouped GEMMs switch to 256-row tiles.
+def test_grouped_small_prefill_tiles(hf):
+    # 96+ rows per expert on average: the grouped GEMMs switch to 192-row prefill
+    # tiles (experts with more rows take several).
     T, d = 1024, SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=58, T=T)
     x = synth.make_x_dev(T, d, seed=58)

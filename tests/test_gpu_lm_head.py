@@ -6,7 +6,7 @@ included).  The library's logits must agree within 1e-2 relative + 2e-3
 absolute, and its greedy token must be the oracle's argmax -- or, where two
 logits are within the tolerance of each other, one of the tied candidates.
 Paths: the T = 1 GEMV with fused argmax, and the grouped GEMM + row argmax for
-batches (128- and 256-row tiles).
+batches (128- and 192-row tiles).
 """
 import ctypes as C
 
