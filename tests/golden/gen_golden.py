@@ -91,13 +91,30 @@ def main() -> None:
         rms.append({"n": n, "seedx": 6000 + i, "seedw": 7000 + i, "eps": 1e-5, "out": bits(y)})
     g["rmsnorm"] = rms
 
+    # The MoE fields of the reference's own test fixture
+    # (tests/fixtures/config_mini.json, read by config.cpp:107-117): hidden 16,
+    # 8 routed experts, top-2, one shared expert, expert intermediate 16, dense
+    # intermediate 48, scale 2.5, normalised weights, topk_group 1.
+    mini_src = "/root/reference/tests/fixtures/config_mini.json"
+    with open(mini_src, encoding="utf-8") as f:
+        fx = json.load(f)
+    keys = ["hidden_size", "intermediate_size", "vocab_size", "num_hidden_layers", "n_routed_experts",
+            "num_experts_per_tok", "n_shared_experts", "moe_intermediate_size", "first_k_dense_replace",
+            "routed_scaling_factor", "norm_topk_prob", "topk_group", "rms_norm_eps", "mlp_layer_types"]
+    g["config_mini"] = {k: fx[k] for k in keys}
+    mini = g["config_mini"]
+
     # Whole moeLayer, flat routing (the reference's rule): the small CPU config
-    # (d=2048, I=1024, 64 experts) for three tokens and the full shape
-    # (d=6144, I=2048, 256 experts) for one token.
+    # (d=2048, I=1024, 64 experts) for three tokens, the full shape (d=6144,
+    # I=2048, 256 experts) for one token, and the fixture's mini config for four.
     layers = []
     for name, spec, tokens in [
         ("small", O.LayerSpec(hidden=2048, inter=1024, n_experts=64, seed=11), 3),
         ("full", O.LayerSpec(hidden=6144, inter=2048, n_experts=256, seed=12), 1),
+        ("config_mini", O.LayerSpec(hidden=mini["hidden_size"], inter=mini["moe_intermediate_size"],
+                                    n_experts=mini["n_routed_experts"], top_k=mini["num_experts_per_tok"],
+                                    n_shared=mini["n_shared_experts"], norm_topk_prob=mini["norm_topk_prob"],
+                                    routed_scaling_factor=mini["routed_scaling_factor"], seed=13), 4),
     ]:
         L = O.SyntheticLayer(spec)
         xs = O.make_x(tokens, spec.hidden, spec.seed)
@@ -107,8 +124,9 @@ def main() -> None:
             if not np.array_equal(out.view(np.uint32), ro.view(np.uint32)):
                 raise SystemExit(f"oracle and reference differ on {name} token {t}")
             layers.append({"name": name, "hidden": spec.hidden, "inter": spec.inter,
-                           "n_experts": spec.n_experts, "top_k": spec.top_k, "seed": spec.seed,
-                           "token": t, "idx": idx.tolist(), "w": bits(w), "out": bits(ro)})
+                           "n_experts": spec.n_experts, "top_k": spec.top_k, "n_shared": spec.n_shared,
+                           "scale": spec.routed_scaling_factor, "norm": spec.norm_topk_prob,
+                           "seed": spec.seed, "token": t, "idx": idx.tolist(), "w": bits(w), "out": bits(ro)})
         L.experts.clear()
     g["moe_layer"] = layers
 

@@ -297,14 +297,25 @@ def test_generator_statistics(oracle_lib):
 
 # ------------------------------------------------------------ MoE layer ----
 
-@pytest.mark.parametrize("which", ["small", "full"])
+def test_config_mini_fixture(golden):
+    # The MoE surface of the reference's own config fixture, as its
+    # tests/test_fixtures.py reads it.
+    m = golden["config_mini"]
+    assert (m["hidden_size"], m["n_routed_experts"], m["num_experts_per_tok"], m["n_shared_experts"],
+            m["moe_intermediate_size"]) == (16, 8, 2, 1, 16)
+    assert m["mlp_layer_types"].count("dense") == m["first_k_dense_replace"] == 1
+    assert m["routed_scaling_factor"] == 2.5 and m["norm_topk_prob"] and m["topk_group"] == 1
+
+
+@pytest.mark.parametrize("which", ["small", "full", "config_mini"])
 def test_moe_layer_bit_exact_vs_reference(oracle_lib, golden, which):
     O = oracle_lib
     cases = [c for c in golden["moe_layer"] if c["name"] == which]
     assert cases
     c0 = cases[0]
     spec = O.LayerSpec(hidden=c0["hidden"], inter=c0["inter"], n_experts=c0["n_experts"],
-                       top_k=c0["top_k"], seed=c0["seed"])
+                       top_k=c0["top_k"], n_shared=c0["n_shared"], norm_topk_prob=c0["norm"],
+                       routed_scaling_factor=c0["scale"], seed=c0["seed"])
     L = O.SyntheticLayer(spec)
     xs = O.make_x(max(c["token"] for c in cases) + 1, spec.hidden, spec.seed)
     for c in cases:
