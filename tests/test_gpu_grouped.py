@@ -91,6 +91,21 @@ def test_grouped_fp32_activations(hf):
     r.free()
 
 
+def test_prefill_tiles_fp32_activations(hf):
+    # Prefill-size tiles with activations that are not BF16-valued: the x lo
+    # half runs as its own sub-step in the gate/up GEMM as well as h's in down.
+    T, d = 1024, SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=64, T=T)
+    xh = O.fill_f32(T * d, 64, 12346, 0.0, 1.0).reshape(T, d)
+    x = capi.DeviceBuffer.of(xh)
+    res = r.forward(x, T)
+    check_dispatch(res, SMALL["n_experts"])
+    for t in range(0, T, 73):
+        r.check_token(xh[t], res, t)
+    x.free()
+    r.free()
+
+
 def test_grouped_without_shared_expert(hf):
     T, d = 16, SMALL["hidden"]
     r = Run(SMALL, n_group=1, topk_group=1, seed=62, T=T, n_shared=0)
