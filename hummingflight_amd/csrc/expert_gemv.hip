@@ -171,13 +171,17 @@ __global__ __launch_bounds__(256) void gateup_t1_kernel(const float* __restrict_
 }
 
 // ICH = 16-byte chunks per lane per down row (I <= 512*ICH).
-// Block b (of G) owns output rows b, b + G, b + 2G, ... (`rows` of them) and
-// has nslots wavefronts; wavefront s keeps h_s in VGPRs and streams those rows
-// of slot s's down matrix, U rows per batch (U*ICH 16-byte loads per lane in
-// flight), writing w_s * (row . h_s) to LDS.  Each output row is then summed
+// Rows go out in batches of U consecutive rows: batch j of block b (of G) is
+// rows j*G*U + b*U .. + U - 1, so each batch of the chip covers G*U
+// consecutive rows (`rows`, a multiple of U, per block).  Block b has nslots
+// wavefronts; wavefront s keeps h_s in VGPRs and streams those rows of slot
+// s's down matrix, one batch at a time (U*ICH 16-byte loads per lane in
+// flight, U*I*2 contiguous bytes), writing w_s * (row . h_s) to LDS.  Each output row is then summed
 // over the slots in a fixed order -- routed slots in rank order, then the
 // shared slices, then `addend` -- the association of glm_forward.cpp:639-640,
 // 658-660 (moeOut += w*y; out = moeOut + sharedOut).
+constexpr int down_batch_rows(int ich) { return 16 / ich > 0 ? 16 / ich : 1; }
+
 template <int ICH>
 __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__ h, LayerDev L,
                                                        Cfg c, const int* __restrict__ sel,
@@ -185,7 +189,7 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
                                                        const float* __restrict__ addend,
                                                        float* __restrict__ out, int nslots,
                                                        int rows) {
-    constexpr int U = (16 / ICH) > 0 ? (16 / ICH) : 1;
+    constexpr int U = down_batch_rows(ICH);
     __shared__ float part[kMaxSlots][kDownMaxRows];
     const int s = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
         u32x4 wv[U][ICH];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int row = b + (i0 + u) * G;
+            const int row = (i0 / U) * G * U + b * U + u;
             if (i0 + u < rows && row < c.d) {
                 const u32x4* r4 = reinterpret_cast<const u32x4*>(sw.dn + (size_t)row * sw.ld);
 #pragma unroll
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int row = b + (i0 + u) * G;
+            const int row = (i0 / U) * G * U + b * U + u;
             if (i0 + u < rows && row < c.d) {
                 float dot = 0.0f;
 #pragma unroll
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
     __syncthreads();
     const int nrouted = c.k < nslots ? c.k : nslots;
     for (int t = threadIdx.x; t < rows; t += blockDim.x) {
-        const int row = b + t * G;
+        const int row = (t / U) * G * U + b * U + t % U;
         if (row >= c.d) continue;
         float moe = 0.0f;
         for (int q = 0; q < nrouted; ++q) moe += part[q][t];
@@ -286,12 +290,15 @@ template <int ICH>
 static hipError_t down_inst(const float* h, const LayerDev& L, const Cfg& c, const int* sel,
                             const float* selw, const float* addend, float* out, int nslots,
                             int blocks, hipStream_t s) {
+    // rows per block: a multiple of the batch (the row mapping covers
+    // [0, grid * rows) exactly then), at most kDownMaxRows.
+    constexpr int U = down_batch_rows(ICH);
+    static_assert(kDownMaxRows % U == 0, "batch");
     int grid = blocks < c.d ? blocks : c.d;
     int rows = (c.d + grid - 1) / grid;
-    if (rows > kDownMaxRows) {
-        rows = kDownMaxRows;
-        grid = (c.d + rows - 1) / rows;
-    }
+    rows = (rows + U - 1) / U * U;
+    if (rows > kDownMaxRows) rows = kDownMaxRows;
+    grid = (c.d + rows - 1) / rows;
     return launch(down_t1_kernel<ICH>, dim3(grid), dim3(64 * nslots), 0, s, h, L, c, sel, selw,
                   addend, out, nslots, rows);
 }
