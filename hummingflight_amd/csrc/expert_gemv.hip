@@ -11,11 +11,11 @@
 //            come first; with in-kernel routing each block ranks the experts
 //            (hf_select.h) while the loads of its wavefronts' first (shared)
 //            rows are in flight, so routing adds no serial step.
-//   down:    one block per set of output rows (interleaved across blocks so
-//            the wavefronts of the chip sweep contiguous memory together),
-//            one wavefront per slot streaming those rows of the slot's down
-//            matrix with h_slot in VGPRs; the per-slot products meet in LDS
-//            and are summed in a fixed order.
+//   down:    one block per set of output rows (groups of U consecutive rows,
+//            interleaved across blocks so each batch of the chip reads one
+//            contiguous stretch of every slot's down matrix), one wavefront
+//            per slot streaming those rows with h_slot in VGPRs; the per-slot
+//            products meet in LDS and are summed in a fixed order.
 // No atomics: every output element has one fixed summation order, so results
 // repeat bit for bit from run to run.
 #include "hf_common.h"
