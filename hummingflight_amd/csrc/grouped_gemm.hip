@@ -39,6 +39,7 @@
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 #include "hf_select.h"
+#include "split_pipeline.h"
 
 #include <type_traits>
 
@@ -427,46 +428,13 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 // of accumulators per lane) cut those re-reads by a third against 256.
 //
 // The lo half of A runs as its own sub-step against the same B stage, so an
-// A stage is always one half (ROWS x 64 BF16): sub-step j = HALVES * s + half
-// multiplies A half `half` of K stage s.  A runs DA sub-steps and B DB K
-// stages ahead; the rings hold RA = DA + 1 A stages and RB = DB + 1 B stages.
-// Column blocks per wavefront: 256-row tiles 4; 192-row tiles 6 for the down
-// projection (384 weight rows) and 4 for gate/up, which leaves LDS for weights
-// two stages ahead.
+// A stage is always one half (ROWS x 64 BF16).  Depths, ring sizes and wait
+// counts: split_pipeline.h.
 template <int EPI, int ROWS>
-constexpr int split_cb() { return ROWS == 256 || EPI == EPI_SWIGLU ? 4 : 6; }
-// Stages ahead (A in sub-steps, B in K stages) and the LDS they take.
-constexpr int split_da(int ROWS, int CB, int H) { return ROWS == 256 && H == 2 ? 2 : 1; }
-constexpr int split_db(int ROWS, int CB, int H) { return CB == 6 || (ROWS == 256 && H == 2) ? 1 : 2; }
-constexpr size_t split_lds(int ROWS, int CB, int H) {
-    return 2 * ((size_t)(split_da(ROWS, CB, H) + 1) * ROWS * GBK + (size_t)(split_db(ROWS, CB, H) + 1) * 64 * CB * GBK);
-}
-constexpr size_t split_lds_max(int ROWS, int CB) {
-    return split_lds(ROWS, CB, 1) > split_lds(ROWS, CB, 2) ? split_lds(ROWS, CB, 1) : split_lds(ROWS, CB, 2);
-}
+constexpr int split_cb() { return split_cb(EPI == EPI_SWIGLU, ROWS); }
 static_assert(split_lds_max(192, 4) <= 160 * 1024 && split_lds_max(192, 6) <= 160 * 1024 &&
                   split_lds_max(256, 4) <= 160 * 1024,
               "LDS");
-
-// DMA instructions a wavefront may leave outstanding at sub-step j (half =
-// j % H) once A(j) and B(j / H) have landed, in the steady issue pattern
-// "sub-step q issues A(q + DA), then B(q / H + DB) when q % H == 0" (loads
-// complete in issue order): those issued after the later of the two.
-constexpr int split_after(int H, int DA, int DB, int half, int NAD, int NBD) {
-    const int s0 = 16;  // any stage past the prologue
-    const int j = s0 * H + half;
-    const int pa = j - DA;         // A(j): first op of sub-step pa
-    const int pb = H * (s0 - DB);  // B(s0): second op of sub-step pb
-    int n = 0, p;
-    if (pa > pb) {
-        p = pa;
-        if (p % H == 0) n += NBD;  // that sub-step's B follows A(j)
-    } else {
-        p = pb;
-    }
-    for (int q = p + 1; q < j; ++q) n += NAD + (q % H == 0 ? NBD : 0);
-    return n;
-}
 
 template <int EPI, int ROWS, int HALVES>
 __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave) {

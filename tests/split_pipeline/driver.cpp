@@ -1,0 +1,22 @@
+// Prints the prefill GEMM pipeline parameters (split_pipeline.h) for every
+// configuration the library instantiates: rows swiglu halves cb da db nad nbd
+// after_half0 after_half1 lds_bytes.
+#include <cstdio>
+
+#include "split_pipeline.h"
+
+int main() {
+    using namespace hf;
+    const int rows_list[] = {192, 256};
+    for (int rows : rows_list)
+        for (int swiglu = 0; swiglu < 2; ++swiglu)
+            for (int h = 1; h <= 2; ++h) {
+                const int cb = split_cb(swiglu != 0, rows);
+                const int da = split_da(rows, cb, h), db = split_db(rows, cb, h);
+                const int nad = rows / 64, nbd = cb;
+                std::printf("%d %d %d %d %d %d %d %d %d %d %zu\n", rows, swiglu, h, cb, da, db, nad, nbd,
+                            split_after(h, da, db, 0, nad, nbd), h == 2 ? split_after(h, da, db, 1, nad, nbd) : -1,
+                            split_lds_max(rows, cb));
+            }
+    return 0;
+}

@@ -1,0 +1,89 @@
+"""Wait counts of the prefill grouped GEMM's DMA pipeline (split_pipeline.h).
+
+The kernel (gemm_item_split, grouped_gemm.hip) issues, per wavefront: a
+prologue of the sub-steps q = -Q .. -1 of the steady pattern, then at each
+sub-step j = H*s + half a wait `s_waitcnt vmcnt(split_after(...))`, a barrier,
+A(j + DA) (NAD DMA instructions) and, on half 0, B(s + DB) (NBD), then the
+multiply of A(j) against B(s).  Indices outside the item load a clamped stage
+into the slot of the unclamped index.  Vector memory loads complete in issue
+order, so the wait is safe when no more than split_after instructions were
+issued after both A(j) and B(s) -- counted here by brute force over whole
+items of 1..9 K stages, for every configuration the library builds (the
+parameters come from the header itself through tests/split_pipeline/driver).
+The ring slots written at sub-step j must not be the ones read at j, and the
+rings must fit the 160 KB of LDS.
+"""
+import os
+import subprocess
+
+import pytest
+
+DRIVER_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "split_pipeline")
+
+
+@pytest.fixture(scope="module")
+def configs():
+    subprocess.run(["make", "-s", "-C", DRIVER_DIR], check=True)
+    out = subprocess.run([os.path.join(DRIVER_DIR, "driver")], capture_output=True, text=True, check=True).stdout
+    rows = [list(map(int, line.split())) for line in out.strip().splitlines()]
+    keys = ["rows", "swiglu", "h", "cb", "da", "db", "nad", "nbd", "after0", "after1", "lds"]
+    return [dict(zip(keys, r)) for r in rows]
+
+
+def simulate(c, nk):
+    """Issue sequence of one item; checks every wait and slot reuse."""
+    H, DA, DB, NAD, NBD = c["h"], c["da"], c["db"], c["nad"], c["nbd"]
+    RA, RB = DA + 1, DB + 1
+    seq = []  # (kind, unclamped index, ops)
+
+    def issue_a(j):
+        seq.append(("A", j, NAD))
+
+    def issue_b(s):
+        seq.append(("B", s, NBD))
+
+    Q = max(DA, H * DB)
+    for q in range(-Q, 0):
+        issue_a(q + DA)
+        if q % H == 0:
+            issue_b(q // H + DB)
+    for s in range(nk):
+        for half in range(H):
+            j = s * H + half
+            ia = [i for i, (k, x, _) in enumerate(seq) if k == "A" and x == j]
+            ib = [i for i, (k, x, _) in enumerate(seq) if k == "B" and x == s]
+            assert len(ia) == 1 and len(ib) == 1
+            later = max(ia[0], ib[0])
+            after = sum(n for (_, _, n) in seq[later + 1:])
+            allowed = c["after0"] if half == 0 else c["after1"]
+            assert 0 <= allowed <= after, (c, nk, j, allowed, after)
+            assert allowed < 64  # vmcnt field
+            # the slots written after the barrier are not the ones multiplied now
+            assert (j + DA) % RA != j % RA
+            if half == 0:
+                assert (s + DB) % RB != s % RB
+            issue_a(j + DA)
+            if half == 0:
+                issue_b(s + DB)
+
+
+def test_every_configuration_is_safe(configs):
+    assert len(configs) == 8
+    for c in configs:
+        assert c["lds"] <= 160 * 1024
+        for nk in range(1, 10):
+            simulate(c, nk)
+
+
+def test_a_count_that_is_one_too_large_is_caught(configs):
+    # The check has teeth: allowing one more outstanding instruction than the
+    # header does breaks at least one configuration.
+    broken = 0
+    for c in configs:
+        bad = dict(c, after0=c["after0"] + 1, after1=c["after1"] + 1 if c["h"] == 2 else -1)
+        try:
+            for nk in range(1, 10):
+                simulate(bad, nk)
+        except AssertionError:
+            broken += 1
+    assert broken == len(configs)
