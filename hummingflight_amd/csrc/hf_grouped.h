@@ -31,8 +31,8 @@ struct GemmArgs {
     int K;                      // reduction length (multiple of 64 * ksplit)
     int N;                      // output columns (SWIGLU: intermediate rows per matrix)
     int n_tiles;                // ceil(N / output columns per tile); SWIGLU: tile_cols / 2 per tile
-    int tile_rows;              // M rows per tile: kGemmTileRows (or 256) or kPrefillTileRows
-    int tile_cols;              // B rows (weight rows) per tile: gemm_tile_cols(tile_rows)
+    int tile_rows;              // M rows per tile: kGemmTileRows, kPrefillTileRows or kDenseTileRows
+    int tile_cols;              // B rows (weight rows) per tile: gemm_tile_cols(tile_rows, epilogue)
     // M tiling: tile i covers rows [tile_row0[i], min(+tile_rows, group_end[tile_group[i]]))
     const int* tile_group;      // null: one group, rows [0, rows_total) in tile_rows-row tiles
     const int* tile_row0;
