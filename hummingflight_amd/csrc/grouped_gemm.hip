@@ -423,9 +423,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 // What bounds these GEMMs is the number of memory requests in flight per CU
 // (each CU's vector L1 holds a limited number of outstanding 128-byte line
 // requests, and at ~640 cycles of average latency that caps a CU near
-// 15 B/cycle), so the tile is as wide as the accumulators allow: every N tile
-// re-reads its M tile's activations, and 384 columns (CB = 6, 144 registers
-// of accumulators per lane) cut those re-reads by a third against 256.
+// 15 B/cycle), so tiles are as wide as registers and LDS allow: every N tile
+// re-reads its M tile's activations, and the down projection's 384 columns
+// (CB = 6, 144 registers of accumulators per lane) cut those re-reads by a
+// third against 256.  Gate/up keeps 256 weight rows (CB = 4) so that its
+// weights run two stages ahead in the LDS; one stage ahead costs it more than
+// the saved re-reads bring.
 //
 // The lo half of A runs as its own sub-step against the same B stage, so an
 // A stage is always one half (ROWS x 64 BF16).  Depths, ring sizes and wait
