@@ -5,7 +5,8 @@
 // p = t*k + r sorted by (expert, p), with per-expert counts and offsets, the
 // same order the CPU oracle's orc_dispatch produces (its stable counting sort).
 //
-// One workgroup of 1024 threads:
+// Small batches, one workgroup of 1024 threads (large batches split steps 1
+// and 3 over pair chunks, see dispatch_count_kernel):
 //   1. histogram of experts (LDS atomics: order cannot matter for counts);
 //   2. block-wide exclusive scans of the counts and of the per-expert M-tile
 //      counts ceil(count_e / tile_rows) -> offsets[E+1] and the M-tile list of
@@ -22,6 +23,9 @@ namespace hf {
 
 constexpr int kDispatchThreads = 1024;
 constexpr int kDispatchWaves = kDispatchThreads / 64;
+// From this many passes of 1024 pairs on, the counting and the scatter run
+// in up to kDispatchMaxChunks workgroups (three launches instead of one).
+constexpr int kDispatchSplitPasses = 8;
 
 // Inclusive scan of v over the 1024 threads of the block (wsum: [16] LDS).
 __device__ __forceinline__ int block_scan(int v, int* wsum) {
@@ -40,28 +44,13 @@ __device__ __forceinline__ int block_scan(int v, int* wsum) {
     return v + before;
 }
 
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
-    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows, int shared_rows,
-    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
-    int* __restrict__ row_token, int* __restrict__ tile_expert, int* __restrict__ tile_row0,
-    int* __restrict__ ntiles_out) {
-    extern __shared__ int smem[];
-    int* cnt = smem;                        // [E]
-    int* cursor = cnt + E;                  // [E]
-    int* whist = cursor + E;                // [waves][E]
-    __shared__ int wsum[kDispatchWaves];
-    __shared__ int totals[2];
+// Offsets, counts and the M-tile list from the per-expert counts cnt[E] (LDS);
+// cursor[e] = offsets[e].  Then the shared group: rows npairs + i <- token i.
+__device__ void dispatch_plan(const int* cnt, int* cursor, int npairs, int E, int tile_rows, int shared_rows,
+                              int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
+                              int* __restrict__ row_token, int* __restrict__ tile_expert,
+                              int* __restrict__ tile_row0, int* __restrict__ ntiles_out, int* wsum, int* totals) {
     const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-
-    for (int e = t; e < E; e += kDispatchThreads) cnt[e] = 0;
-    __syncthreads();
-    for (int p = t; p < npairs; p += kDispatchThreads) {
-        const int e = min(max(idx[p], 0), E - 1);
-        atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
     // Scans over experts in chunks of 1024 (E <= 1024 in practice: one chunk).
     int run_rows = 0, run_tiles = 0;
     for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
@@ -90,7 +79,6 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         run_tiles += totals[1];
         __syncthreads();
     }
-    // The shared group: rows npairs + i <- token i.
     const int shared_tiles = (shared_rows + tile_rows - 1) / tile_rows;
     for (int j = t; j < shared_tiles; j += kDispatchThreads) {
         tile_expert[run_tiles + j] = E;
@@ -106,13 +94,22 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
         *ntiles_out = run_tiles + shared_tiles;
     }
     __syncthreads();
+}
 
+// Stable scatter of pairs [begin, end), 1024 per pass in pair order: a pair's
+// slot is cursor[e] + (same-expert pairs in earlier wavefronts of the pass) +
+// (same-expert pairs in earlier lanes of its wavefront); cursor (LDS) advances.
+__device__ void dispatch_scatter(const int* __restrict__ idx, int begin, int end, int k, int E, int key_bits,
+                                 int* cursor, int* whist, int* __restrict__ perm, int* __restrict__ row_token) {
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = 0; base < npairs; base += kDispatchThreads) {
+    for (int base = begin; base < end; base += kDispatchThreads) {
         for (int i = t; i < kDispatchWaves * E; i += kDispatchThreads) whist[i] = 0;
         __syncthreads();
         const int p = base + t;
-        const bool valid = p < npairs;
+        const bool valid = p < end;
         const int e = valid ? min(max(idx[p], 0), E - 1) : 0;
         uint64_t same = __ballot(valid);
         for (int b = 0; b < key_bits; ++b) {
@@ -140,22 +137,130 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     }
 }
 
+// Histogram of experts over pairs [begin, end) into cnt[E] (LDS atomics:
+// order cannot matter for counts).
+__device__ void dispatch_count(const int* __restrict__ idx, int begin, int end, int E, int* cnt) {
+    for (int e = threadIdx.x; e < E; e += kDispatchThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int p = begin + (int)threadIdx.x; p < end; p += kDispatchThreads) atomicAdd(&cnt[min(max(idx[p], 0), E - 1)], 1);
+    __syncthreads();
+}
+
+// Small batches: everything in one workgroup.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
+    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows, int shared_rows,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
+    int* __restrict__ row_token, int* __restrict__ tile_expert, int* __restrict__ tile_row0,
+    int* __restrict__ ntiles_out) {
+    extern __shared__ int smem[];
+    int* cnt = smem;              // [E]
+    int* cursor = cnt + E;        // [E]
+    int* whist = cursor + E;      // [waves][E]
+    __shared__ int wsum[kDispatchWaves];
+    __shared__ int totals[2];
+    dispatch_count(idx, 0, npairs, E, cnt);
+    dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
+                  tile_row0, ntiles_out, wsum, totals);
+    dispatch_scatter(idx, 0, npairs, k, E, key_bits, cursor, whist, perm, row_token);
+}
+
+// Large batches, step 1 of 3: workgroup b counts the experts of pair chunk b
+// (pairs [b * chunk, (b + 1) * chunk)) into chunk_hist[b][E].
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(const int* __restrict__ idx, int npairs,
+                                                                          int E, int chunk,
+                                                                          int* __restrict__ chunk_hist) {
+    extern __shared__ int smem[];
+    const int b = blockIdx.x;
+    dispatch_count(idx, b * chunk, min(npairs, (b + 1) * chunk), E, smem);
+    for (int e = threadIdx.x; e < E; e += kDispatchThreads) chunk_hist[(size_t)b * E + e] = smem[e];
+}
+
+// Step 2: one workgroup sums the chunk counts, plans offsets and tiles, and
+// turns chunk_hist[b][e] into the first slot of chunk b's expert-e pairs.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
+    int nchunks, int npairs, int E, int tile_rows, int shared_rows, int* __restrict__ chunk_hist,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm, int* __restrict__ row_token,
+    int* __restrict__ tile_expert, int* __restrict__ tile_row0, int* __restrict__ ntiles_out) {
+    extern __shared__ int smem[];
+    int* cnt = smem;        // [E]
+    int* cursor = cnt + E;  // [E]
+    __shared__ int wsum[kDispatchWaves];
+    __shared__ int totals[2];
+    for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
+        int c = 0;
+        for (int b = 0; b < nchunks; ++b) c += chunk_hist[(size_t)b * E + e];
+        cnt[e] = c;
+    }
+    __syncthreads();
+    dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
+                  tile_row0, ntiles_out, wsum, totals);
+    for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
+        int run = cursor[e];
+        for (int b = 0; b < nchunks; ++b) {
+            const int c = chunk_hist[(size_t)b * E + e];
+            chunk_hist[(size_t)b * E + e] = run;
+            run += c;
+        }
+    }
+}
+
+// Step 3: workgroup b scatters chunk b from its first slots.
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_scatter_kernel(
+    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int chunk,
+    const int* __restrict__ chunk_base, int* __restrict__ perm, int* __restrict__ row_token) {
+    extern __shared__ int smem[];
+    int* cursor = smem;        // [E]
+    int* whist = cursor + E;   // [waves][E]
+    const int b = blockIdx.x;
+    for (int e = threadIdx.x; e < E; e += kDispatchThreads) cursor[e] = chunk_base[(size_t)b * E + e];
+    __syncthreads();
+    dispatch_scatter(idx, b * chunk, min(npairs, (b + 1) * chunk), k, E, key_bits, cursor, whist, perm, row_token);
+}
+
+static hipError_t raise_lds(const void* fn, size_t lds, size_t& raised) {
+    if (lds <= 48 * 1024 || lds <= raised) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) raised = lds;
+    return e;
+}
+
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
                            int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, hipStream_t s) {
+                           int* tile_row0, int* ntiles, int* chunk_hist, hipStream_t s) {
     int bits = 1;
     while ((1 << bits) < E) ++bits;
+    const int npairs = T * k;
     const size_t lds = sizeof(int) * (size_t)E * (2 + kDispatchWaves);
-    static size_t lds_raised = 0;
-    if (lds > 48 * 1024 && lds > lds_raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(dispatch_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const int passes = (npairs + kDispatchThreads - 1) / kDispatchThreads;
+    if (passes < kDispatchSplitPasses || !chunk_hist) {
+        static size_t raised = 0;
+        hipError_t e = raise_lds(reinterpret_cast<const void*>(dispatch_kernel), lds, raised);
         if (e != hipSuccess) return e;
-        lds_raised = lds;
+        return launch(dispatch_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds, s, idx, npairs, k, E, bits,
+                      tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert, tile_row0, ntiles);
     }
-    return launch(dispatch_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds, s, idx, T * k, k,
-                  E, bits, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
-                  tile_row0, ntiles);
+    // One chunk of whole passes per workgroup, at most kDispatchMaxChunks chunks.
+    const int per = (passes + kDispatchMaxChunks - 1) / kDispatchMaxChunks;
+    const int chunk = per * kDispatchThreads;
+    const int nchunks = (npairs + chunk - 1) / chunk;
+    static size_t raised_count = 0, raised_plan = 0, raised_scatter = 0;
+    const size_t lds_count = sizeof(int) * (size_t)E, lds_plan = 2 * sizeof(int) * (size_t)E,
+                 lds_scatter = sizeof(int) * (size_t)E * (1 + kDispatchWaves);
+    hipError_t e = raise_lds(reinterpret_cast<const void*>(dispatch_count_kernel), lds_count, raised_count);
+    if (e == hipSuccess) e = raise_lds(reinterpret_cast<const void*>(dispatch_plan_kernel), lds_plan, raised_plan);
+    if (e == hipSuccess)
+        e = raise_lds(reinterpret_cast<const void*>(dispatch_scatter_kernel), lds_scatter, raised_scatter);
+    if (e == hipSuccess)
+        e = launch(dispatch_count_kernel, dim3(nchunks), dim3(kDispatchThreads), (uint32_t)lds_count, s, idx, npairs, E,
+                   chunk, chunk_hist);
+    if (e == hipSuccess)
+        e = launch(dispatch_plan_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds_plan, s, nchunks, npairs, E,
+                   tile_rows, shared_rows, chunk_hist, counts, offsets, perm, row_token, tile_expert, tile_row0,
+                   ntiles);
+    if (e == hipSuccess)
+        e = launch(dispatch_scatter_kernel, dim3(nchunks), dim3(kDispatchThreads), (uint32_t)lds_scatter, s, idx,
+                   npairs, k, E, bits, chunk, static_cast<const int*>(chunk_hist), perm, row_token);
+    return e;
 }
 
 }  // namespace hf

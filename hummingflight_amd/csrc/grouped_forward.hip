@@ -51,7 +51,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
+                    w.chunk_hist, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -80,6 +80,7 @@ int grouped_workspace_alloc() {
         {(void**)&w.tile_expert, sizeof(int) * w.max_tiles},
         {(void**)&w.tile_row0, sizeof(int) * w.max_tiles},
         {(void**)&w.ntiles, 256},
+        {(void**)&w.chunk_hist, sizeof(int) * (size_t)kDispatchMaxChunks * c.E},
         {(void**)&w.lo_flag, 256},
         {(void**)&w.xh, 2 * (size_t)T * c.d},
         {(void**)&w.xl, 2 * (size_t)T * c.d},
@@ -145,7 +146,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     prof_begin(p, "dispatch", s);
     HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, TR, shared_rows, w.counts,
                                     w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0,
-                                    w.ntiles, s),
+                                    w.ntiles, w.chunk_hist, s),
                     "dispatch");
 
     // Gate/up of every group: the routed experts' (token, rank) rows and the

@@ -70,9 +70,12 @@ hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, con
 // Stable counting sort of the T*k (token, rank) pairs by expert plus the M-tile
 // list (tile_rows rows per tile) of the grouped GEMM.  With shared_rows > 0 a
 // group E of shared_rows rows (sorted rows T*k + t <- token t) follows the
-// experts: the shared expert multiplied in the same launches.
+// experts: the shared expert multiplied in the same launches.  chunk_hist
+// ([kDispatchMaxChunks, E] ints, or null) lets large batches count and
+// scatter in several workgroups.
+constexpr int kDispatchMaxChunks = 64;
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
                            int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, hipStream_t s);
+                           int* tile_row0, int* ntiles, int* chunk_hist, hipStream_t s);
 
 }  // namespace hf
