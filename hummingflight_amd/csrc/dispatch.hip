@@ -188,6 +188,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
     __shared__ int totals[2];
     for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
         int c = 0;
+#pragma unroll 8
         for (int b = 0; b < nchunks; ++b) c += chunk_hist[(size_t)b * E + e];
         cnt[e] = c;
     }
@@ -196,6 +197,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
                   tile_row0, ntiles_out, wsum, totals);
     for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
         int run = cursor[e];
+#pragma unroll 8
         for (int b = 0; b < nchunks; ++b) {
             const int c = chunk_hist[(size_t)b * E + e];
             chunk_hist[(size_t)b * E + e] = run;
