@@ -49,8 +49,10 @@ __device__ __forceinline__ int block_scan(int v, int* wsum) {
 __device__ void dispatch_plan(const int* cnt, int* cursor, int npairs, int E, int tile_rows, int shared_rows,
                               int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
                               int* __restrict__ row_token, int* __restrict__ tile_expert,
-                              int* __restrict__ tile_row0, int* __restrict__ ntiles_out, int* wsum, int* totals) {
+                              int* __restrict__ tile_row0, int* __restrict__ ntiles_out,
+                              unsigned* __restrict__ item_ctr, int* wsum, int* totals) {
     const int t = threadIdx.x;
+    if (item_ctr && t < kItemCounters) item_ctr[t] = 0u;  // the grouped GEMMs' work counters
     // Scans over experts in chunks of 1024 (E <= 1024 in practice: one chunk).
     int run_rows = 0, run_tiles = 0;
     for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows, int shared_rows,
     int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
     int* __restrict__ row_token, int* __restrict__ tile_expert, int* __restrict__ tile_row0,
-    int* __restrict__ ntiles_out) {
+    int* __restrict__ ntiles_out, unsigned* __restrict__ item_ctr) {
     extern __shared__ int smem[];
     int* cnt = smem;              // [E]
     int* cursor = cnt + E;        // [E]
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     __shared__ int totals[2];
     dispatch_count(idx, 0, npairs, E, cnt);
     dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
-                  tile_row0, ntiles_out, wsum, totals);
+                  tile_row0, ntiles_out, item_ctr, wsum, totals);
     dispatch_scatter(idx, 0, npairs, k, E, key_bits, cursor, whist, perm, row_token);
 }
 
@@ -180,7 +182,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(const 
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
     int nchunks, int npairs, int E, int tile_rows, int shared_rows, int* __restrict__ chunk_hist,
     int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm, int* __restrict__ row_token,
-    int* __restrict__ tile_expert, int* __restrict__ tile_row0, int* __restrict__ ntiles_out) {
+    int* __restrict__ tile_expert, int* __restrict__ tile_row0, int* __restrict__ ntiles_out,
+    unsigned* __restrict__ item_ctr) {
     extern __shared__ int smem[];
     int* cnt = smem;        // [E]
     int* cursor = cnt + E;  // [E]
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
     }
     __syncthreads();
     dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
-                  tile_row0, ntiles_out, wsum, totals);
+                  tile_row0, ntiles_out, item_ctr, wsum, totals);
     for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
         int run = cursor[e];
 #pragma unroll 8
@@ -228,7 +231,7 @@ static hipError_t raise_lds(const void* fn, size_t lds, size_t& raised) {
 
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
                            int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, int* chunk_hist, hipStream_t s) {
+                           int* tile_row0, int* ntiles, int* chunk_hist, unsigned* item_ctr, hipStream_t s) {
     int bits = 1;
     while ((1 << bits) < E) ++bits;
     const int npairs = T * k;
@@ -239,7 +242,8 @@ hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, i
         hipError_t e = raise_lds(reinterpret_cast<const void*>(dispatch_kernel), lds, raised);
         if (e != hipSuccess) return e;
         return launch(dispatch_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds, s, idx, npairs, k, E, bits,
-                      tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert, tile_row0, ntiles);
+                      tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert, tile_row0, ntiles,
+                      item_ctr);
     }
     // One chunk of whole passes per workgroup, at most kDispatchMaxChunks chunks.
     const int per = (passes + kDispatchMaxChunks - 1) / kDispatchMaxChunks;
@@ -258,7 +262,7 @@ hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, i
     if (e == hipSuccess)
         e = launch(dispatch_plan_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds_plan, s, nchunks, npairs, E,
                    tile_rows, shared_rows, chunk_hist, counts, offsets, perm, row_token, tile_expert, tile_row0,
-                   ntiles);
+                   ntiles, item_ctr);
     if (e == hipSuccess)
         e = launch(dispatch_scatter_kernel, dim3(nchunks), dim3(kDispatchThreads), (uint32_t)lds_scatter, s, idx,
                    npairs, k, E, bits, chunk, static_cast<const int*>(chunk_hist), perm, row_token);

@@ -51,7 +51,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.chunk_hist, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
+                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -81,6 +81,7 @@ int grouped_workspace_alloc() {
         {(void**)&w.tile_row0, sizeof(int) * w.max_tiles},
         {(void**)&w.ntiles, 256},
         {(void**)&w.chunk_hist, sizeof(int) * (size_t)kDispatchMaxChunks * c.E},
+        {(void**)&w.item_ctr, sizeof(unsigned) * kItemCounters},
         {(void**)&w.lo_flag, 256},
         {(void**)&w.xh, 2 * (size_t)T * c.d},
         {(void**)&w.xl, 2 * (size_t)T * c.d},
@@ -146,7 +147,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     prof_begin(p, "dispatch", s);
     HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, TR, shared_rows, w.counts,
                                     w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0,
-                                    w.ntiles, w.chunk_hist, s),
+                                    w.ntiles, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
                     "dispatch");
 
     // Gate/up of every group: the routed experts' (token, rank) rows and the
@@ -172,6 +173,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.h_hi = w.hh;
     gu.h_lo = w.hl;
     gu.ksplit = 1;
+    gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
 
@@ -196,6 +198,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.out_f32 = w.y;
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
+    dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
 

@@ -598,13 +598,43 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
-    for (int li = r.begin; li < r.end; li += r.stride) {
-        const int item = r.item(li);
+    auto run = [&](int item) {
         if (LOM != kLoNone && use_lo)
             gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
         else
             gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave);
         __syncthreads();
+    };
+    if (!a.item_ctr || !r.by_mtile) {
+        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li));
+        return;
+    }
+    // Dynamic: each XCD's workgroups take the items of the XCD's M tiles in
+    // order from a counter (zeroed by the dispatch), then help the other XCDs
+    // with theirs, so the kernel ends when the last item does, not when the
+    // workgroup dealt the most items does.  Every grab advances a counter and
+    // each counter stops yielding at its XCD's item count: the loop ends.
+    __shared__ int next_item;
+    int probe = 0;
+    for (;;) {
+        if (t == 0) {
+            int got = -1;
+            while (got < 0 && probe < r.nxcd) {
+                const int x = (r.xcd + probe) % r.nxcd;
+                const int li = (int)atomicAdd(a.item_ctr + x, 1u);
+                const int n = (m_tiles - x + r.nxcd - 1) / r.nxcd * r.per_m;
+                if (li < n)
+                    got = (x + r.nxcd * (li / r.per_m)) * r.per_m + li % r.per_m;
+                else
+                    ++probe;
+            }
+            next_item = got;
+        }
+        __syncthreads();
+        const int item = next_item;
+        __syncthreads();
+        if (item < 0) break;
+        run(item);
     }
 }
 

@@ -38,6 +38,7 @@ struct GroupedWorkspace {
     int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
     int* ntiles = nullptr;       // [1] M tiles in use
     int* chunk_hist = nullptr;   // [kDispatchMaxChunks, E] dispatch chunk counts / first slots
+    unsigned* item_ctr = nullptr;  // [kItemCounters] prefill GEMM work counters (zeroed by the dispatch)
     unsigned int* lo_flag = nullptr;  // [1] x has a nonzero BF16 lo half
     uint16_t* xh = nullptr;      // [maxT, d] x BF16 hi (token order)
     uint16_t* xl = nullptr;      // [maxT, d] x BF16 lo

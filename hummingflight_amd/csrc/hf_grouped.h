@@ -57,6 +57,7 @@ struct GemmArgs {
     uint16_t* h_lo;
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
+    unsigned* item_ctr;         // prefill kernel: 8 zeroed per-XCD item counters (null: static items)
 };
 
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s);
@@ -73,9 +74,13 @@ hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, con
 // experts: the shared expert multiplied in the same launches.  chunk_hist
 // ([kDispatchMaxChunks, E] ints, or null) lets large batches count and
 // scatter in several workgroups.
+// The dispatch also zeroes item_ctr[kItemCounters] (or nothing when null):
+// the per-XCD work counters of the gate/up (first 8) and down (last 8)
+// prefill GEMMs that follow it.
 constexpr int kDispatchMaxChunks = 64;
+constexpr int kItemCounters = 16;
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
                            int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, int* chunk_hist, hipStream_t s);
+                           int* tile_row0, int* ntiles, int* chunk_hist, unsigned* item_ctr, hipStream_t s);
 
 }  // namespace hf
