@@ -173,7 +173,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.h_hi = w.hh;
     gu.h_lo = w.hl;
     gu.ksplit = 1;
-    gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;
+    gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
 

@@ -590,30 +590,14 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     }
 }
 
-template <int EPI, int LOM, int ROWS>
-__global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t slds[];  // split_lds_max(ROWS, CB) bytes
+// Dynamic items of the prefill kernel: each XCD's workgroups take the items of
+// the XCD's M tiles in order from a counter (zeroed by the dispatch), then help
+// the other XCDs with theirs, so the kernel ends when the last item does, not
+// when the workgroup dealt the most items does.  Every grab advances a counter
+// and each counter stops yielding at its XCD's item count: the loop ends.
+template <class Run>
+__device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange& r, int m_tiles, Run&& run) {
     const int t = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
-    const ItemRange r = item_range<true>(a, m_tiles);
-    const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
-    auto run = [&](int item) {
-        if (LOM != kLoNone && use_lo)
-            gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
-        else
-            gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave);
-        __syncthreads();
-    };
-    if (!a.item_ctr || !r.by_mtile) {
-        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li));
-        return;
-    }
-    // Dynamic: each XCD's workgroups take the items of the XCD's M tiles in
-    // order from a counter (zeroed by the dispatch), then help the other XCDs
-    // with theirs, so the kernel ends when the last item does, not when the
-    // workgroup dealt the most items does.  Every grab advances a counter and
-    // each counter stops yielding at its XCD's item count: the loop ends.
     __shared__ int next_item;
     int probe = 0;
     for (;;) {
@@ -636,6 +620,30 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
         if (item < 0) break;
         run(item);
     }
+}
+
+template <int EPI, int LOM, int ROWS>
+__global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t slds[];  // split_lds_max(ROWS, CB) bytes
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
+    const ItemRange r = item_range<true>(a, m_tiles);
+    const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
+    auto run = [&](int item) {
+        if (LOM != kLoNone && use_lo)
+            gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
+        else
+            gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave);
+        __syncthreads();
+    };
+    // 256-row tiles fill the whole 160 KB of LDS, leaving none for the
+    // dynamic loop's shared item slot: they always take static items.
+    if (ROWS != kPrefillTileRows || !a.item_ctr || !r.by_mtile) {
+        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li));
+        return;
+    }
+    if constexpr (ROWS == kPrefillTileRows) dynamic_items(a, r, m_tiles, run);
 }
 
 // out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):

@@ -57,7 +57,7 @@ struct GemmArgs {
     uint16_t* h_lo;
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
-    unsigned* item_ctr;         // prefill kernel: 8 zeroed per-XCD item counters (null: static items)
+    unsigned* item_ctr;         // 8 zeroed per-XCD work counters (null: static items; see run_items_dynamic)
 };
 
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s);
@@ -76,7 +76,7 @@ hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, con
 // scatter in several workgroups.
 // The dispatch also zeroes item_ctr[kItemCounters] (or nothing when null):
 // the per-XCD work counters of the gate/up (first 8) and down (last 8)
-// prefill GEMMs that follow it.
+// grouped GEMMs that follow it.
 constexpr int kDispatchMaxChunks = 64;
 constexpr int kItemCounters = 16;
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
