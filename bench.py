@@ -18,7 +18,8 @@ against its roofline as `roofline` (durations from the kernels' own dispatch
 timestamps, recorded on the launch stream during a second pass of the timed
 steps), and the reference CPU path timed on this host as `cpu_baseline`.
 
-    python bench.py [--steps K] [--warmup W] [--workload decode|batched|prefill|streamed|copy]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload decode|batched|prefill|streamed|streamed_cached|dense|lm_head|load|copy]
 """
 from __future__ import annotations
 
