@@ -199,12 +199,17 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
 // its quarter of B stage s+D (DMA into the ring slot stage s-1 used), and
 // multiplies stage s.  A and B of one stage are issued together, so waiting
 // for stage s (in-order load counter) never waits for a later stage.
-template <int EPI, bool USE_LO, int WAVES>
+// NRB: this wavefront's 16-row blocks that hold rows (0, 1 or 2), fixed per
+// instantiation so that a wavefront loads A fragments only for rows that
+// exist (the activation requests otherwise take up to a third of the CU's
+// queue of outstanding requests at batched-decode sizes) while every load
+// count stays a compile-time constant for the counter waits.
+template <int EPI, bool USE_LO, int WAVES, int NRB>
 __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* ring, int t, int wave) {
     constexpr int GBM = 32 * WAVES;     // tile rows: 32 per wavefront
     constexpr int BJ = 16 / WAVES;      // 1 KB weight DMAs per wave per stage
     constexpr int cols_per_tile = EPI == EPI_SWIGLU ? GBN / 2 : GBN;
-    constexpr int NA = USE_LO ? 8 : 4;  // A loads per wave per stage
+    constexpr int NA = NRB * (USE_LO ? 4 : 2);  // A loads per wave per stage
     constexpr int D = USE_LO ? kDepthLo : kDepthHi;
     constexpr int RING = D + 1;
     const int lane = t & 63;
@@ -232,9 +237,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
         b1 = a.b_fixed1;
     }
     const int kbase = ks * Kc;
-    // 16-row blocks of this wavefront that hold rows (0, 1 or 2; wave-uniform).
-    const int wrows = min(max(rows - 32 * wave, 0), 32);
-    const int nrb = (wrows + 15) >> 4;
+    constexpr int nrb = NRB;
 
     // A fragment sources: lane row fr of row blocks 0 and 1, clamped to the
     // tile's last row (rows past it are loaded but never multiplied or stored).
@@ -283,7 +286,7 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
     auto load_a = [&](AFrag& f, int s) {
         s = min(s, nk - 1);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) {
                 f[0][rb][kh] = ld_global(ap[rb] + s * GBK + kh * 32);
@@ -394,12 +397,28 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 
     for (int li = r.begin; li < r.end; li += r.stride) {
         const int item = r.item(li);
+        // Row blocks of this wavefront in the item's tile (wave-uniform).
+        const int mt = item / a.ksplit / a.n_tiles;
+        const int g = a.tile_group ? a.tile_group[mt] : 0;
+        const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * 32 * WAVES;
+        const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
+        const int wrows = min(max(min(32 * WAVES, row_end - row0) - 32 * wave, 0), 32);
+        const int nrb = (wrows + 15) >> 4;
+        auto run = [&](auto lo_c) {
+            constexpr bool LO = decltype(lo_c)::value;
+            if (nrb == 2)
+                gemm_item<EPI, LO, WAVES, 2>(a, item, ring, t, wave);
+            else if (nrb == 1)
+                gemm_item<EPI, LO, WAVES, 1>(a, item, ring, t, wave);
+            else
+                gemm_item<EPI, LO, WAVES, 0>(a, item, ring, t, wave);
+        };
         if constexpr (LOM == kLoAlways)
-            gemm_item<EPI, true, WAVES>(a, item, ring, t, wave);
+            run(std::true_type{});
         else if (LOM == kLoByFlag && use_lo)
-            gemm_item<EPI, LOM == kLoByFlag, WAVES>(a, item, ring, t, wave);
+            run(std::integral_constant<bool, LOM == kLoByFlag>{});
         else
-            gemm_item<EPI, false, WAVES>(a, item, ring, t, wave);
+            run(std::false_type{});
         __syncthreads();  // all DMA landed and all ring reads done before the next item
     }
 }
