@@ -198,6 +198,25 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
     const int nch = c.I >> 3;
     const bool routed = s < c.k;
     const SlotW sw = slot_weights(L, c, s, routed ? sel[s] : 0);
+
+    // The first batch's weight loads go out before h and the slot weight,
+    // which they do not depend on.
+    u32x4 wv[U][ICH];
+    auto load_batch = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int row = (i0 / U) * G * U + b * U + u;
+            if (i0 + u < rows && row < c.d) {
+                const u32x4* r4 = reinterpret_cast<const u32x4*>(sw.dn + (size_t)row * sw.ld);
+#pragma unroll
+                for (int jj = 0; jj < ICH; ++jj) {
+                    const int ch = lane + 64 * jj;
+                    if (ch < nch) wv[u][jj] = ld_stream(r4 + ch);
+                }
+            }
+        }
+    };
+    load_batch(0);
     const float ws = routed && selw ? selw[s] : 1.0f;
 
     float hv[ICH][8];
@@ -216,19 +235,7 @@ __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__
     }
 
     for (int i0 = 0; i0 < rows; i0 += U) {
-        u32x4 wv[U][ICH];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int row = (i0 / U) * G * U + b * U + u;
-            if (i0 + u < rows && row < c.d) {
-                const u32x4* r4 = reinterpret_cast<const u32x4*>(sw.dn + (size_t)row * sw.ld);
-#pragma unroll
-                for (int jj = 0; jj < ICH; ++jj) {
-                    const int ch = lane + 64 * jj;
-                    if (ch < nch) wv[u][jj] = ld_stream(r4 + ch);
-                }
-            }
-        }
+        if (i0 > 0) load_batch(i0);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int row = (i0 / U) * G * U + b * U + u;
