@@ -6,6 +6,9 @@ bit-exact given the GPU's router logits, and outputs within 1e-2 relative +
 2e-3 absolute of the oracle's per-token moeLayer (or, at sizes where the oracle
 would take minutes, of the T=1 decode path, itself pinned to the oracle).
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -174,6 +177,29 @@ def test_prefill_4096_uniform_routing(hf):
     check_vs_decode(r, x, res, range(7, T, 128), d)
     xh = x.download(np.float32, T * d).reshape(T, d)
     for t in (0, 2047, 4095):
+        r.check_token(xh[t], res, t)
+    x.free()
+    r.free()
+
+
+def test_prefill_4096_zipf_hot_experts(hf):
+    # Prefill chunk with Zipf(1.1)-skewed routing: hot experts span several
+    # 192-row tiles, cold ones leave their one tile mostly empty.
+    with open(os.path.join(os.path.dirname(__file__), "golden", "zipf_bias_e256.json")) as fh:
+        zb = json.load(fh)
+    T, d, E = 4096, FULL["hidden"], FULL["n_experts"]
+    seed = zb["layer_seed"]
+    r = Run(FULL, n_group=8, topk_group=4, seed=seed, T=T, bias=np.array(zb["bias"], np.float32))
+    x = synth.make_x_dev(T, d, seed=seed)
+    res = r.forward(x, T)
+    counts = check_dispatch(res, E)
+    assert counts.max() > 2 * 192 and counts.min() < 96
+    check_selection(r, res, T)
+    hot = np.argsort(-counts)[:2]
+    rows = [t for t in range(T) if np.isin(res["idx"][t], hot).any()]
+    check_vs_decode(r, x, res, rows[:: max(1, len(rows) // 16)] + list(range(11, T, 256)), d)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    for t in (rows[0], rows[-1], 4095):
         r.check_token(xh[t], res, t)
     x.free()
     r.free()
