@@ -9,7 +9,8 @@
 //
 // T = 1: a persistent GEMV.  Each block stages the normalised hidden state in
 //   LDS; each wavefront streams whole vocabulary rows, two at a time, 16-byte
-//   loads (lane l: elements 512j + 8l .. +7); lane 0 writes the logit and
+//   non-temporal loads (lane l: elements 512j + 8l .. +7; the weights are read
+//   once and kept out of the caches' way); lane 0 writes the logit and
 //   keeps the wavefront's running winner, the block merges its four, and one
 //   small launch merges the blocks' winners (lowest row on equal values).
 // T > 1: the grouped GEMM (one group, fixed B = lm_head) writes the logits,
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(kLmBlock) void lm_gemv_kernel(const uint16_t* __res
 #pragma unroll
             for (int j = 0; j < KCH; ++j) {
                 const int k0 = j * 512 + lane * 8;
-                w[u][j] = k0 < K ? *reinterpret_cast<const u32x4*>(row + k0) : (u32x4){0, 0, 0, 0};
+                w[u][j] = k0 < K ? ld_stream(reinterpret_cast<const u32x4*>(row + k0)) : (u32x4){0, 0, 0, 0};
             }
         }
         float acc[RF];
