@@ -22,13 +22,27 @@ __global__ __launch_bounds__(256) void router_t1_kernel(const float* __restrict_
     const int e = blockIdx.x;
     const int t = threadIdx.x;
     const uint16_t* row = L.router + (size_t)e * c.d;
+    // hidden <= 8192: at most 4 chunks of 8 per thread, all loads issued
+    // before the first product.
+    constexpr int kMaxCh = 8192 / 8 / 256;
+    u32x4 w[kMaxCh];
+    float4 xa[kMaxCh], xb[kMaxCh];
+#pragma unroll
+    for (int j = 0; j < kMaxCh; ++j) {
+        const int ch = t + 256 * j;
+        if (ch * 8 < c.d) {
+            w[j] = ld_plain(reinterpret_cast<const u32x4*>(row) + ch);
+            xa[j] = reinterpret_cast<const float4*>(x)[2 * ch];
+            xb[j] = reinterpret_cast<const float4*>(x)[2 * ch + 1];
+        }
+    }
     float acc = 0.0f;
-    for (int ch = t; ch * 8 < c.d; ch += 256) {
-        const u32x4 w = ld_plain(reinterpret_cast<const u32x4*>(row) + ch);
-        const float4 xa = reinterpret_cast<const float4*>(x)[2 * ch];
-        const float4 xb = reinterpret_cast<const float4*>(x)[2 * ch + 1];
-        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        acc = dot8(w, xv, acc);
+#pragma unroll
+    for (int j = 0; j < kMaxCh; ++j) {
+        if ((t + 256 * j) * 8 < c.d) {
+            const float xv[8] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w, xb[j].x, xb[j].y, xb[j].z, xb[j].w};
+            acc = dot8(w[j], xv, acc);
+        }
     }
     acc = wave_sum(acc);
     if ((t & 63) == 0) red[t >> 6] = acc;
