@@ -109,6 +109,50 @@ def test_prefill_tiles_fp32_activations(hf):
     r.free()
 
 
+@pytest.mark.parametrize("T", [767, 768])
+def test_tile_size_switch_boundary(hf, T):
+    # 64 experts, top-8: T*k >= 96*E switches to 192-row tiles at T = 768.
+    d = SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=90 + T % 2, T=T)
+    x = synth.make_x_dev(T, d, seed=90 + T % 2)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    check_dispatch(res, SMALL["n_experts"])
+    check_selection(r, res, T)
+    for t in range(0, T, 97):
+        r.check_token(xh[t], res, t)
+    x.free()
+    r.free()
+
+
+PREFILL_EDGE = [
+    # hidden 960: the last 384-column down tile is partial; inter 320: so is
+    # the last gate/up tile (128 h columns per tile); 32 experts, top-4, so
+    # T = 800 gives 100 rows per expert on average (192-row tiles).
+    ("partial_n_tiles_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 1),
+    ("partial_n_tiles_no_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 0),
+    ("top1_many_rows", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 1),
+]
+
+
+@pytest.mark.parametrize("name,dims,n_group,topk_group,n_shared", PREFILL_EDGE, ids=[e[0] for e in PREFILL_EDGE])
+def test_prefill_tiles_edge_shapes(hf, name, dims, n_group, topk_group, n_shared):
+    T = 800
+    r = Run(dims, n_group=n_group, topk_group=topk_group, seed=95, T=T, n_shared=n_shared)
+    x = synth.make_x_dev(T, dims["hidden"], seed=95)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * dims["hidden"]).reshape(T, -1)
+    counts = check_dispatch(res, dims["n_experts"])
+    assert T * dims["top_k"] >= 96 * dims["n_experts"]  # the 192-row tile path
+    if dims["top_k"] == 1:
+        assert counts.max() > 192  # experts over several tiles
+    for t in range(0, T, 41):
+        r.check_token(xh[t], res, t)
+    check_vs_decode(r, x, res, range(3, T, 160), dims["hidden"])
+    x.free()
+    r.free()
+
+
 def test_grouped_without_shared_expert(hf):
     T, d = 16, SMALL["hidden"]
     r = Run(SMALL, n_group=1, topk_group=1, seed=62, T=T, n_shared=0)
