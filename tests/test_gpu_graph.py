@@ -1,0 +1,85 @@
+"""The MoE forward captured into a HIP graph and replayed.
+
+A serving loop may capture a layer (or a chain of layers) once and replay it.
+The forward issues only kernel launches on the caller's stream -- no memsets,
+no host synchronisation, no allocation -- so stream capture records it
+whole.  Every replay is checked bit for bit against the same call made
+eagerly, with other eager work on the stream between replays, at T = 1
+(decode kernels), T = 37 (128-row grouped GEMM) and T = 1024 (192-row tiles,
+multi-workgroup dispatch, per-XCD work counters that the dispatch zeroes on
+every replay).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from hummingflight_amd import capi, synth
+from moe_harness import SMALL, Run
+
+pytestmark = pytest.mark.gpu
+
+CAPTURE_MODE_RELAXED = 2
+
+
+def hip():
+    lib = C.CDLL("libamdhip64.so")
+    for name in ("hipStreamCreate", "hipStreamDestroy", "hipStreamSynchronize", "hipStreamBeginCapture",
+                 "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy",
+                 "hipGraphDestroy"):
+        getattr(lib, name).restype = C.c_int
+    return lib
+
+
+def ok(rc, what):
+    assert rc == 0, f"{what} failed with HIP error {rc}"
+
+
+@pytest.mark.parametrize("T", [1, 37, 1024])
+def test_forward_replays_from_hip_graph(hf, T):
+    d = SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=80 + T % 7, T=T)
+    x = synth.make_x_dev(T, d, seed=80 + T % 7)
+    x2 = synth.make_x_dev(T, d, seed=81 + T % 7)
+    out_e = capi.DeviceBuffer(T * d * 4)
+    out_g = capi.DeviceBuffer(T * d * 4)
+    fwd = capi.load().hfmoe_moe_forward
+    h = hip()
+    s = C.c_void_p()
+    ok(h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        capi.check(fwd(0, x.ptr, T, out_e.ptr, s))
+        ok(h.hipStreamSynchronize(s), "sync")
+        ref = out_e.download(np.float32, T * d).copy()
+
+        ok(h.hipStreamBeginCapture(s, CAPTURE_MODE_RELAXED), "hipStreamBeginCapture")
+        rc = fwd(0, x.ptr, T, out_g.ptr, s)
+        ok(h.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
+        capi.check(rc)
+        ok(h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+
+        for rep in range(4):
+            capi.call("hfmoe_memset", out_g.ptr, 0, T * d * 4)
+            ok(h.hipGraphLaunch(exe, s), "hipGraphLaunch")
+            ok(h.hipStreamSynchronize(s), "sync")
+            got = out_g.download(np.float32, T * d)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"replay {rep} differs from eager"
+            # Other work through the same workspace between replays.
+            capi.check(fwd(0, x2.ptr, T, out_e.ptr, s))
+            ok(h.hipStreamSynchronize(s), "sync")
+        other = out_e.download(np.float32, T * d)
+        assert not np.array_equal(other, ref)
+        # The token's output is still the oracle's (selection and tolerance).
+        res = r.forward(x, T)
+        assert np.array_equal(res["out"].reshape(-1).view(np.uint32), ref.view(np.uint32))
+        r.check_token(x.download(np.float32, d), res, 0)
+    finally:
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamDestroy(s)
+        for b in (x, x2, out_e, out_g):
+            b.free()
+        r.free()
