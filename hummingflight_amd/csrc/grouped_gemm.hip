@@ -673,18 +673,19 @@ __global__ void combine_kernel(const float* __restrict__ wts, const float* __res
     const int d4 = d >> 2;
     if (i4 >= (size_t)T * d4) return;
     const int t = (int)(i4 / d4), n4 = (int)(i4 % d4);
-    const float4* y4 = reinterpret_cast<const float4*>(y);
+    // y is read once: non-temporal loads.
+    const f32x4_t* y4 = reinterpret_cast<const f32x4_t*>(y);
     float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int r = 0; r < k; ++r) {
         const float w = wts[(size_t)t * k + r];
-        const float4 v = y4[((size_t)t * k + r) * d4 + n4];
+        const f32x4_t v = __builtin_nontemporal_load(y4 + ((size_t)t * k + r) * d4 + n4);
         m.x += w * v.x;
         m.y += w * v.y;
         m.z += w * v.z;
         m.w += w * v.w;
     }
     if (shared_row0 >= 0) {
-        const float4 v = y4[((size_t)shared_row0 + t) * d4 + n4];
+        const f32x4_t v = __builtin_nontemporal_load(y4 + ((size_t)shared_row0 + t) * d4 + n4);
         m.x += v.x;
         m.y += v.y;
         m.z += v.z;
@@ -693,11 +694,36 @@ __global__ void combine_kernel(const float* __restrict__ wts, const float* __res
     reinterpret_cast<float4*>(out)[i4] = m;
 }
 
-// x FP32 [n] -> BF16 hi/lo; *flag |= 1 when any lo is nonzero.
+// x FP32 [n] -> BF16 hi/lo; *flag |= 1 when any lo is nonzero.  Eight values
+// per thread and step (two 16-byte loads, one 16-byte store per half) when x
+// is 16-byte aligned, then single values for the rest.  x is read once:
+// non-temporal loads; hi/lo are read again by the GEMMs that follow.
 __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ hi,
                                   uint16_t* __restrict__ lo, size_t n, unsigned* __restrict__ flag) {
     bool nz = false;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(hi) |
+                       reinterpret_cast<uintptr_t>(lo)) & 15) == 0;
+    const size_t n8 = vec ? n / 8 : 0;
+    for (size_t i = tid; i < n8; i += stride) {
+        const f32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(x) + 2 * i);
+        const f32x4_t b = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(x) + 2 * i + 1);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t h0 = f32_to_bf16(v[2 * q]), h1 = f32_to_bf16(v[2 * q + 1]);
+            const uint32_t l0 = f32_to_bf16(v[2 * q] - __uint_as_float(h0 << 16));
+            const uint32_t l1 = f32_to_bf16(v[2 * q + 1] - __uint_as_float(h1 << 16));
+            hw[q] = h0 | (h1 << 16);
+            lw[q] = l0 | (l1 << 16);
+            nz |= ((l0 | l1) & 0x7FFFu) != 0;
+        }
+        reinterpret_cast<u32x4*>(hi)[i] = (u32x4){hw[0], hw[1], hw[2], hw[3]};
+        reinterpret_cast<u32x4*>(lo)[i] = (u32x4){lw[0], lw[1], lw[2], lw[3]};
+    }
+    for (size_t i = n8 * 8 + tid; i < n; i += stride) {
         const float v = x[i];
         const uint16_t h = f32_to_bf16(v);
         const uint16_t l = f32_to_bf16(v - __uint_as_float((uint32_t)h << 16));
