@@ -25,6 +25,7 @@
 
 #include <cctype>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <dirent.h>
 #include <memory>
@@ -262,7 +263,7 @@ bool open_shard(hfmoe_checkpoint& ck, const std::string& path, const std::map<st
         return false;
     }
     sh->data0 = n + 8;
-    if (sh->data0 + 8 > sh->size) {
+    if (n > sh->size - 8 || sh->data0 + 8 > sh->size) {  // n + 8 must not wrap
         err = path + ": header length exceeds the file";
         return false;
     }
@@ -313,8 +314,13 @@ bool open_shard(hfmoe_checkpoint& ck, const std::string& path, const std::map<st
                     ok = false;
                     break;
                 }
-                ref.shape.push_back((int64_t)dim.num);
-                numel *= (uint64_t)dim.num;
+                const uint64_t dn = (uint64_t)dim.num;
+                if (dn && numel > UINT64_MAX / dn) {  // the product must not wrap
+                    ok = false;
+                    break;
+                }
+                ref.shape.push_back((int64_t)dn);
+                numel *= dn;
             }
         }
         if (!ok) {
@@ -322,8 +328,11 @@ bool open_shard(hfmoe_checkpoint& ck, const std::string& path, const std::map<st
             continue;
         }
         const JVal* off = t.get("data_offsets");
+        // Offsets past the file are out of bounds; checking them as doubles
+        // first keeps the integer conversion and data0 + end from wrapping.
         ok = off && off->kind == JVal::ARR && off->arr.size() == 2 && off->arr[0].kind == JVal::NUM &&
-             off->arr[1].kind == JVal::NUM && off->arr[0].num >= 0.0;
+             off->arr[1].kind == JVal::NUM && off->arr[0].num >= 0.0 && off->arr[0].num <= off->arr[1].num &&
+             off->arr[1].num <= (double)sh->size;
         if (ok) {
             ref.begin = (uint64_t)off->arr[0].num;
             ref.end = (uint64_t)off->arr[1].num;

@@ -70,6 +70,11 @@ CASES = [
     ("fractional_dim", tensor_entry("BF16", [1.5], 0, 8), "w", 8, "shape_rejected"),
     ("scalar_shape", tensor_entry("BF16", [], 0, 2), "w", 8, "shape_rejected"),
     ("empty_span", tensor_entry("BF16", [0], 0, 0), "w", 8, "bounds_rejected"),
+    # Not in the reference's list: inputs whose arithmetic would wrap 64 bits.
+    # 20 * 5581 * 384773 * 429509837 = 2^64 + 4, so a wrapping element count
+    # would match the 8-byte span.
+    ("shape_product_wraps", tensor_entry("BF16", [20, 5581, 384773, 429509837], 0, 8), "w", 8, "shape_rejected"),
+    ("offsets_past_the_file", tensor_entry("BF16", [4], 1e30, 1e30 + 8), "w", 8, "bounds_rejected"),
 ]
 
 
@@ -102,6 +107,25 @@ def test_duplicate_name_second_rejected(tmp_path):
     rc, t = info(ck, "w")
     assert rc == capi.OK and t.file_offset == len(raw_shard(hdr, 0))  # the first entry's data (begin 0)
     close(ck)
+
+
+def test_offsets_near_2_pow_64_rejected(tmp_path):
+    # With a header of 4 KB or more, data start + end would wrap past 2^64 to a
+    # place inside the file for these offsets (2048 bytes apart, both exact
+    # doubles): the span must be rejected as out of bounds, not accepted.
+    entry = tensor_entry("BF16", [1024], 2**64 - 4096, 2**64 - 2048)
+    hdr = json.dumps({"__metadata__": {"pad": "x" * 4200}, "w": entry})
+    rc, ck = one(tmp_path, "wrap.safetensors", raw_shard(hdr, 64))
+    assert rc == capi.OK
+    s = stats(ck)
+    assert (s["total"], s["accepted"], s["bounds_rejected"]) == (1, 0, 1), s
+    close(ck)
+
+
+def test_header_length_near_2_pow_64_fails(tmp_path):
+    rc, ck = one(tmp_path, "huge.safetensors", (2**64 - 8).to_bytes(8, "little") + b"{}" + b" " * 14)
+    assert rc == capi.ERR_INVALID_ARGUMENT
+    assert b"header" in capi.load().hfmoe_last_error()
 
 
 def unaligned_header():
