@@ -439,10 +439,11 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 // re-reads its weights).  ROWS = 256 for one-group GEMMs (dense layers, LM
 // head), whose weights are re-read once per M tile.
 //
-// What bounds these GEMMs is the number of memory requests in flight per CU
-// (each CU's vector L1 holds a limited number of outstanding 128-byte line
-// requests, and at ~640 cycles of average latency that caps a CU near
-// 15 B/cycle), so tiles are as wide as registers and LDS allow: every N tile
+// What bounds these GEMMs is the rate of memory requests per CU: ~67-77
+// outstanding 128-byte line requests at ~680-730 cycles of average latency,
+// i.e. 12-15 B per cycle, at the ~1.8-2.0 GHz the GPU runs under this MFMA
+// load; activation re-reads (L2 hits) are a third of those requests.  So
+// tiles are as wide as registers and LDS allow: every N tile
 // re-reads its M tile's activations, and the down projection's 384 columns
 // (CB = 6, 144 registers of accumulators per lane) cut those re-reads by a
 // third against 256.  Gate/up keeps 256 weight rows (CB = 4) so that its
