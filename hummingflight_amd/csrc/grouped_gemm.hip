@@ -746,8 +746,18 @@ __global__ void router_reduce_kernel(const float* __restrict__ part, int ksplit,
                                      float2* __restrict__ scores) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= T * E) return;
+    const size_t st = (size_t)T * E;
+    // Eight partials loaded at a time, summed in split order.
     float s = 0.0f;
-    for (int q = 0; q < ksplit; ++q) s += part[(size_t)q * T * E + i];
+    int q = 0;
+    for (; q + 8 <= ksplit; q += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(part + (q + u) * st + i);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; q < ksplit; ++q) s += part[q * st + i];
     logits[i] = s;
     scores[i] = score_pair(s, bias, i % E);
 }
