@@ -8,9 +8,16 @@ forward over one token; inputs are already in HBM when the timed region starts.
 Other workloads of the same layer:
   batched   T=64 tokens, correction bias calibrated for Zipf(1.1) expert
             popularity (tests/golden/zipf_bias_e256.json); HBM-bound
-  prefill   T=4096 tokens, near-uniform routing (bias ~N(0,0.001)); MFMA-bound
+  prefill   T=4096 tokens, near-uniform routing (bias ~N(0,0.001)); HBM
+            roofline, MFMA fraction beside it
   streamed  8 chained layers (RMSNorm + MoE + residual), T=1, routed experts in
             pinned host RAM, the selected ones copied to HBM on a side stream
+  streamed_cached  the same with an HBM expert cache and next-layer copy-ahead
+  dense     a dense-MLP layer (intermediate 12288), T=1 or --dense-tokens
+  lm_head   final norm + LM head (vocab 154880) + greedy argmax, T=1
+  load      a MoE layer from a safetensors shard into HBM (GB/s)
+  plugin    the per-expert plugin calls: stage an expert, expert FFN with
+            host buffers (calls/s)
   copy      counter calibration (4 GiB device-to-device copies)
 
 Prints one JSON line: tokens/s as `value`, the dominant kernel's achieved rate
@@ -19,7 +26,7 @@ timestamps, recorded on the launch stream during a second pass of the timed
 steps), and the reference CPU path timed on this host as `cpu_baseline`.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload decode|batched|prefill|streamed|streamed_cached|dense|lm_head|load|copy]
+                    [--workload decode|batched|prefill|streamed|streamed_cached|dense|lm_head|load|plugin|copy]
 """
 from __future__ import annotations
 
@@ -559,6 +566,53 @@ def run_load(args) -> None:
                                  "routed_experts": E, "shared_experts": 1}}), flush=True)
 
 
+def run_plugin(args) -> None:
+    """Per-expert plugin surface (gpuExpertStage / gpuExpertFFN, cuda_backend.h:64-85)
+    at the full expert shape: staging distinct experts from pageable host
+    memory into the HBM expert cache, then synchronous expert FFN calls on a
+    resident expert with host x and out (the reference's blocking contract:
+    x up, FFN, out back, per call)."""
+    d, I = FULL["hidden"], FULL["inter"]
+    n_stage = 12
+    ebytes = 3 * d * I * 2
+    rng = np.random.default_rng(args.seed)
+    w = (rng.standard_normal(3 * d * I, dtype=np.float32) * 0.02).view(np.uint32)
+    w = ((w + 0x7FFF + ((w >> 16) & 1)) >> 16).astype(np.uint16)  # BF16, round to nearest even
+    x = rng.standard_normal(d, dtype=np.float32)
+    out = np.zeros(d, np.float32)
+    L = capi.load()
+    capi.call("hfmoe_expert_cache_config", n_stage + 4, 2)
+    capi.call("hfmoe_expert_stage", 0, 0, w.ctypes.data, d, I)  # first call: slot pool set-up
+    capi.call("hfmoe_synchronize")
+    t0 = time.perf_counter()
+    for e in range(1, n_stage + 1):
+        capi.call("hfmoe_expert_stage", 0, e, w.ctypes.data, d, I)
+    capi.call("hfmoe_synchronize")
+    t_stage = (time.perf_counter() - t0) / n_stage
+    ffn = L.hfmoe_expert_ffn
+    for _ in range(args.warmup):
+        capi.check(ffn(0, 1, x.ctypes.data, out.ctypes.data, d, I))
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        capi.check(ffn(0, 1, x.ctypes.data, out.ctypes.data, d, I))
+    t_ffn = (time.perf_counter() - t0) / args.steps
+    L.hfmoe_expert_cache_shutdown()
+    gbs = ebytes / t_ffn / 1e9
+    print(json.dumps({"metric": "per-expert plugin: expert FFN calls/s (host x/out, blocking) + stage GB/s, "
+                                "d=6144, I=2048",
+                      "value": round(1.0 / t_ffn, 1), "unit": "calls/s", "n_gpus": 1, "steps": args.steps,
+                      "warmup": args.warmup, "us_per_call": round(t_ffn * 1e6, 2), "higher_is_better": True,
+                      "dtype": "bf16", "data": "synthetic",
+                      "roofline": {"bound": "hbm", "kernel": "expert_ffn (gate/up + down GEMV, one expert)",
+                                   "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                   "note": "whole call: x H2D, two kernels, out D2H and the synchronisation"},
+                      "stage": {"experts": n_stage, "bytes_each": ebytes, "ms_each": round(t_stage * 1e3, 3),
+                                "gbs": round(ebytes / t_stage / 1e9, 2),
+                                "source": "pageable numpy buffer, copied through pinned staging slots"},
+                      "config": {"workload": "expert_plugin", "hidden": d, "moe_intermediate": I}}), flush=True)
+
+
 def run_copy(args) -> None:
     """Counter calibration: 4 GiB device-to-device copies (HIP's own copy kernel)."""
     n = 4 << 30
@@ -608,7 +662,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "dense", "lm_head",
-                             "load", "copy"])
+                             "load", "plugin", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
@@ -630,13 +684,13 @@ def main() -> int:
         return 2
     defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
                 "streamed_cached": (30, 10), "dense": (100, 10), "lm_head": (100, 10), "load": (1, 0),
-                "copy": (5, 0)}
+                "plugin": (200, 20), "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
     args.warmup = d_warm if args.warmup is None else args.warmup
     capi.call("hfmoe_init", 0)
-    if args.workload in ("copy", "load"):
-        (run_copy if args.workload == "copy" else run_load)(args)
+    if args.workload in ("copy", "load", "plugin"):
+        {"copy": run_copy, "load": run_load, "plugin": run_plugin}[args.workload](args)
         capi.load().hfmoe_shutdown()
         return 0
     if args.workload == "decode":

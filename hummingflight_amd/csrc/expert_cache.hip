@@ -36,6 +36,7 @@ struct ExpertCache {
     float* x = nullptr;
     float* h = nullptr;
     float* out = nullptr;
+    float* io_pin = nullptr;              // pinned [2, hidden]: x, then out, of an FFN call
     uint64_t clock = 0;
     std::unordered_map<uint64_t, int> where;
 
@@ -60,7 +61,8 @@ struct ExpertCache {
         if (x) hipFree(x);
         if (h) hipFree(h);
         if (out) hipFree(out);
-        x = h = out = nullptr;
+        if (io_pin) hipHostFree(io_pin);
+        x = h = out = io_pin = nullptr;
         where.clear();
         allocated = false;
     }
@@ -86,6 +88,8 @@ struct ExpertCache {
         if (e == hipSuccess) e = hipMalloc(&x, sizeof(float) * hd);
         if (e == hipSuccess) e = hipMalloc(&h, sizeof(float) * it);
         if (e == hipSuccess) e = hipMalloc(&out, sizeof(float) * hd);
+        if (e == hipSuccess)
+            e = hipHostMalloc(reinterpret_cast<void**>(&io_pin), 2 * sizeof(float) * hd, hipHostMallocDefault);
         if (e != hipSuccess) {
             release();
             return fail(HFMOE_ERR_OUT_OF_MEMORY, "expert cache allocation failed: %s", hipGetErrorString(e));
@@ -221,16 +225,21 @@ int hfmoe_expert_ffn(int layer, int expert_id, const float* x, float* out, int h
         d.pending = false;
     }
     const size_t half = (size_t)hidden * inter;
-    e = hipMemcpyAsync(c.x, x, sizeof(float) * hidden, hipMemcpyHostToDevice, s);
+    // x and out cross PCIe through the pinned io buffer: DMA copies, rather
+    // than the driver's staged copies of pageable memory.
+    const size_t xb = sizeof(float) * hidden;
+    memcpy(c.io_pin, x, xb);
+    e = hipMemcpyAsync(c.x, c.io_pin, xb, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return fail_hip(e, "H2D x");
-    g.pcie_bytes += sizeof(float) * hidden;
+    g.pcie_bytes += xb;
     e = launch_expert_ffn(d.w, d.w + half, d.w + 2 * half, c.x, c.h, c.out, hidden, inter,
                           gu_blocks(), dn_blocks(), s);
     if (e != hipSuccess) return fail_hip(e, "expert ffn launch");
-    e = hipMemcpyAsync(out, c.out, sizeof(float) * hidden, hipMemcpyDeviceToHost, s);
+    e = hipMemcpyAsync(c.io_pin + hidden, c.out, xb, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail_hip(e, "D2H out");
-    g.pcie_bytes += sizeof(float) * hidden;
+    memcpy(out, c.io_pin + hidden, xb);
+    g.pcie_bytes += xb;
     return HFMOE_OK;
 }
 
