@@ -208,6 +208,24 @@ def test_grouped_full_shape_batch_invariance(hf):
     r.free()
 
 
+def test_grouped_full_shape_t2560(hf):
+    # 2560 tokens: 128-row tiles still, and the router GEMM splits K 12 ways
+    # (its reduction takes partials eight at a time, then the rest).
+    T, d = 2560, FULL["hidden"]
+    r = Run(FULL, n_group=8, topk_group=4, seed=68, T=T)
+    x = synth.make_x_dev(T, d, seed=68)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    check_dispatch(res, FULL["n_experts"])
+    check_selection(r, res, T)
+    for t in (0, 1, 1279, 2559):
+        ref = r.ref.logits(xh[t])
+        assert np.max(np.abs(ref - res["logits"][t])) < 1e-4 * max(1.0, np.max(np.abs(ref)))
+    check_vs_decode(r, x, res, range(9, T, 320), d)
+    x.free()
+    r.free()
+
+
 def test_prefill_4096_uniform_routing(hf):
     # Prefill chunk: near-uniform routing (bias ~N(0, 0.001)), ~128 rows per expert.
     T, d, E = 4096, FULL["hidden"], FULL["n_experts"]
