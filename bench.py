@@ -156,6 +156,20 @@ def run_decode(args) -> dict:
         "ms_per_step_with_kernel_events": sec_prof * 1e3,
         "kernels": kernels,
     }
+    # The reference's host contract (moeLayer: host float[hidden] in and out,
+    # synchronous), PCIe copies included; a note beside `value`, not `value`.
+    xh = x.download(np.float32, shape.hidden).copy()
+    oh = np.zeros(shape.hidden, np.float32)
+    host = capi.load().hfmoe_moe_layer
+
+    def host_step():
+        rc = host(0, xh.ctypes.data, oh.ctypes.data)
+        if rc:
+            capi.check(rc)
+
+    sec_host = time_steps(host_step, args.steps, args.warmup)
+    res["host_contract"] = {"us_per_call": round(sec_host * 1e6, 2), "tokens_per_s": round(1.0 / sec_host, 1),
+                            "note": "hfmoe_moe_layer: x host -> HBM, layer, out -> host, synchronised per call"}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_decode(shape, args.seed, args.cpu_seconds)
     layer.free()

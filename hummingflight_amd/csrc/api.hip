@@ -96,6 +96,7 @@ static void free_workspace() {
     void* ptrs[] = {w.logits, w.scores, w.idx, w.wts, w.h, w.counter, w.x_io, w.out_io, w.tmp};
     for (void* p : ptrs)
         if (p) hipFree(p);
+    if (w.io_pin) hipHostFree(w.io_pin);
     w = Workspace{};
 }
 
@@ -127,7 +128,17 @@ static int alloc_workspace() {
                         a.bytes, hipGetErrorString(e));
         }
     }
-    hipError_t e = hipMemset(w.counter, 0, 256);
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&w.io_pin), 2 * sizeof(float) * (size_t)c.d,
+                                 hipHostMallocCoherent | hipHostMallocMapped);
+    if (e != hipSuccess) {
+        free_workspace();
+        return fail(HFMOE_ERR_OUT_OF_MEMORY, "pinned io buffer: %s", hipGetErrorString(e));
+    }
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&w.io_pin_dev), w.io_pin, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        w.io_pin_dev = nullptr;
+    }
+    e = hipMemset(w.counter, 0, 256);
     if (e != hipSuccess) return fail_hip(e, "hipMemset(counter)");
     return HFMOE_OK;
 }
@@ -349,15 +360,27 @@ int hfmoe_moe_layer(int layer, const float* input_host, float* output_host) {
     int rc = require_cfg();
     if (rc) return rc;
     if (!input_host || !output_host) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null buffer");
+    // x and out cross PCIe through the coherent pinned io buffer, read and
+    // written by a small kernel on the compute stream (no DMA-engine round
+    // trip per 24 KB), or by DMA copies where the buffer has no device address.
     const size_t bytes = sizeof(float) * (size_t)g.cfg.d;
-    hipError_t e = hipMemcpyAsync(g.ws.x_io, input_host, bytes, hipMemcpyHostToDevice, g.stream);
+    float* pin = g.ws.io_pin;
+    float* pin_dev = g.ws.io_pin_dev;
+    memcpy(pin, input_host, bytes);
+    hipError_t e = pin_dev ? launch_copy_f32(pin_dev, g.ws.x_io, g.cfg.d, g.stream)
+                           : hipMemcpyAsync(g.ws.x_io, pin, bytes, hipMemcpyHostToDevice, g.stream);
     if (e != hipSuccess) return fail_hip(e, "H2D input");
     g.pcie_bytes += bytes;
     rc = hfmoe_moe_forward(layer, g.ws.x_io, 1, g.ws.out_io, nullptr);
-    if (rc) return rc;
-    e = hipMemcpyAsync(output_host, g.ws.out_io, bytes, hipMemcpyDeviceToHost, g.stream);
+    if (rc) {
+        hipStreamSynchronize(g.stream);  // the pinned buffer is reused by the next call
+        return rc;
+    }
+    e = pin_dev ? launch_copy_f32(g.ws.out_io, pin_dev + g.cfg.d, g.cfg.d, g.stream)
+                : hipMemcpyAsync(pin + g.cfg.d, g.ws.out_io, bytes, hipMemcpyDeviceToHost, g.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
     if (e != hipSuccess) return fail_hip(e, "D2H output");
+    memcpy(output_host, pin + g.cfg.d, bytes);
     g.pcie_bytes += bytes;
     return HFMOE_OK;
 }

@@ -37,7 +37,8 @@ struct ExpertCache {
     float* x = nullptr;
     float* h = nullptr;
     float* out = nullptr;
-    float* io_pin = nullptr;              // pinned [2, hidden]: x, then out, of an FFN call
+    float* io_pin = nullptr;              // pinned coherent [2, hidden]: x, then out, of an FFN call
+    float* io_pin_dev = nullptr;          // its device address (null: DMA copies instead)
     uint64_t clock = 0;
     std::unordered_map<uint64_t, int> where;
 
@@ -63,7 +64,7 @@ struct ExpertCache {
         if (h) hipFree(h);
         if (out) hipFree(out);
         if (io_pin) hipHostFree(io_pin);
-        x = h = out = io_pin = nullptr;
+        x = h = out = io_pin = io_pin_dev = nullptr;
         where.clear();
         allocated = false;
     }
@@ -90,7 +91,12 @@ struct ExpertCache {
         if (e == hipSuccess) e = hipMalloc(&h, sizeof(float) * it);
         if (e == hipSuccess) e = hipMalloc(&out, sizeof(float) * hd);
         if (e == hipSuccess)
-            e = hipHostMalloc(reinterpret_cast<void**>(&io_pin), 2 * sizeof(float) * hd, hipHostMallocDefault);
+            e = hipHostMalloc(reinterpret_cast<void**>(&io_pin), 2 * sizeof(float) * hd,
+                              hipHostMallocCoherent | hipHostMallocMapped);
+        if (e == hipSuccess && hipHostGetDevicePointer(reinterpret_cast<void**>(&io_pin_dev), io_pin, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            io_pin_dev = nullptr;
+        }
         if (e != hipSuccess) {
             release();
             return fail(HFMOE_ERR_OUT_OF_MEMORY, "expert cache allocation failed: %s", hipGetErrorString(e));
@@ -247,17 +253,20 @@ int hfmoe_expert_ffn(int layer, int expert_id, const float* x, float* out, int h
         d.pending = false;
     }
     const size_t half = (size_t)hidden * inter;
-    // x and out cross PCIe through the pinned io buffer: DMA copies, rather
-    // than the driver's staged copies of pageable memory.
+    // x and out cross PCIe through the coherent pinned io buffer, read and
+    // written by a small kernel on the compute stream (or by DMA copies where
+    // the buffer has no device address).
     const size_t xb = sizeof(float) * hidden;
     memcpy(c.io_pin, x, xb);
-    e = hipMemcpyAsync(c.x, c.io_pin, xb, hipMemcpyHostToDevice, s);
+    e = c.io_pin_dev ? launch_copy_f32(c.io_pin_dev, c.x, hidden, s)
+                     : hipMemcpyAsync(c.x, c.io_pin, xb, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return fail_hip(e, "H2D x");
     g.pcie_bytes += xb;
     e = launch_expert_ffn(d.w, d.w + half, d.w + 2 * half, c.x, c.h, c.out, hidden, inter,
                           gu_blocks(), dn_blocks(), s);
     if (e != hipSuccess) return fail_hip(e, "expert ffn launch");
-    e = hipMemcpyAsync(c.io_pin + hidden, c.out, xb, hipMemcpyDeviceToHost, s);
+    e = c.io_pin_dev ? launch_copy_f32(c.out, c.io_pin_dev + hidden, hidden, s)
+                     : hipMemcpyAsync(c.io_pin + hidden, c.out, xb, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail_hip(e, "D2H out");
     memcpy(out, c.io_pin + hidden, xb);

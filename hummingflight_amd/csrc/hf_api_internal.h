@@ -24,6 +24,8 @@ struct Workspace {
     unsigned int* counter = nullptr;
     float* x_io = nullptr;       // [d]  host-contract staging
     float* out_io = nullptr;     // [d]
+    float* io_pin = nullptr;     // pinned host [2, d], coherent: the host contract's x, then out
+    float* io_pin_dev = nullptr; // its device address (null: copies go through hipMemcpyAsync)
     float* tmp = nullptr;        // [2, maxT, d] (mlp block: normed x, MoE out)
 };
 
@@ -175,5 +177,6 @@ void stream_pool_release();
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s);
 hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s);
+hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s);
 
 }  // namespace hf

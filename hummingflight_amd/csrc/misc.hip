@@ -56,6 +56,19 @@ __global__ void add_inplace_kernel(float* __restrict__ dst, const float* __restr
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] += src[i];
 }
 
+// n floats from src to dst, either of which may be mapped host memory: a
+// small transfer done by the compute queue, without a DMA-engine round trip.
+__global__ void copy_f32_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 64) blocks = 64;
+    return launch(copy_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+}
+
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s) {
     if (d > 8 * kNormThreads) return hipErrorInvalidValue;
