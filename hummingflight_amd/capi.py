@@ -115,6 +115,7 @@ _SIGS = [
     ("hfmoe_embedding_gather", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
     ("hfmoe_matvec_bf16_dev", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     ("hfmoe_argmax_rows", C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    ("hfmoe_router_sigmoid", C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
     ("hfmoe_lm_head", C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("hfmoe_dense_mlp_forward", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_expert_cache_config", C.c_int, [C.c_int, C.c_int]),

@@ -155,6 +155,13 @@ int require_cfg() {
     return HFMOE_OK;
 }
 
+int check_align(int layer, const char* what, const void* p, size_t align) {
+    if (reinterpret_cast<uintptr_t>(p) % align)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: %s weights at %p are not %zu-byte aligned", layer, what, p,
+                    align);
+    return HFMOE_OK;
+}
+
 int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     if (!v || !*v) return dflt;
@@ -238,6 +245,8 @@ int hfmoe_configure(const hfmoe_config* cfg) {
     int rc = require_init();
     if (rc) return rc;
     if (!cfg) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null config");
+    // A rejected configuration leaves the earlier one in force; once the old
+    // workspace is released below, only a fully allocated new one counts.
     Cfg c{};
     c.d = cfg->hidden;
     c.I = cfg->moe_intermediate;
@@ -266,6 +275,9 @@ int hfmoe_configure(const hfmoe_config* cfg) {
         return fail(HFMOE_ERR_UNSUPPORTED, "n_shared_experts=%d too large", c.n_shared);
     if ((size_t)(c.k + c.n_shared) * c.I * sizeof(float) > 160 * 1024)
         return fail(HFMOE_ERR_UNSUPPORTED, "(k + n_shared) * I FP32 activations exceed LDS");
+    if (cfg->max_tokens < 0 || cfg->max_tokens > kMaxTokens)
+        return fail(HFMOE_ERR_UNSUPPORTED, "max_tokens=%d: must be in 0..%d", cfg->max_tokens, kMaxTokens);
+    g.configured = false;
     g.cfg = c;
     g.max_tokens = cfg->max_tokens > 0 ? cfg->max_tokens : 1;
     g.vram_budget = cfg->vram_budget_bytes;
@@ -278,7 +290,10 @@ int hfmoe_configure(const hfmoe_config* cfg) {
     rc = alloc_workspace();
     if (rc) return rc;
     rc = grouped_workspace_alloc();
-    if (rc) return rc;
+    if (rc) {
+        free_workspace();
+        return rc;
+    }
     g.configured = true;
     return HFMOE_OK;
 }
@@ -296,6 +311,21 @@ int hfmoe_register_layer(int layer, const hfmoe_layer_weights* w) {
                     w->experts_location);
     for (int i = 0; i < 3 * c.E; ++i)
         if (!w->experts[i]) return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: expert pointer %d is NULL", layer, i);
+    // Alignment the kernels' loads need: 16 bytes for every BF16 matrix read
+    // from HBM (16-byte vector loads and LDS DMA), 4 for the F32 bias, 2 for the
+    // norm weight.  Host-pinned experts are copied by the DMA engines into the
+    // library's own slots, which carry no requirement.
+    rc = check_align(layer, "router", w->router_dev, 16);
+    if (!rc && c.n_shared > 0) rc = check_align(layer, "shared gate", w->shared_gate_dev, 16);
+    if (!rc && c.n_shared > 0) rc = check_align(layer, "shared up", w->shared_up_dev, 16);
+    if (!rc && c.n_shared > 0) rc = check_align(layer, "shared down", w->shared_down_dev, 16);
+    if (!rc) rc = check_align(layer, "e_score_correction_bias", w->score_bias_dev, 4);
+    if (!rc) rc = check_align(layer, "post_attention_norm", w->post_attention_norm_dev, 2);
+    for (int i = 0; !rc && w->experts_location == HFMOE_EXPERTS_DEVICE && i < 3 * c.E; ++i)
+        if (reinterpret_cast<uintptr_t>(w->experts[i]) & 15)
+            rc = fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: HBM expert %d %s weights at %p are not 16-byte aligned",
+                      layer, i / 3, i % 3 == 0 ? "gate" : i % 3 == 1 ? "up" : "down", (const void*)w->experts[i]);
+    if (rc) return rc;
     auto it = g.layers.find(layer);
     if (it != g.layers.end() && it->second.etab_dev) hipFree(it->second.etab_dev);
     g.pool.policy.forget_layer(layer);  // cached HBM copies hold the old weights
@@ -364,6 +394,8 @@ int hfmoe_moe_layer(int layer, const float* input_host, float* output_host) {
     // written by a small kernel on the compute stream (no DMA-engine round
     // trip per 24 KB), or by DMA copies where the buffer has no device address.
     const size_t bytes = sizeof(float) * (size_t)g.cfg.d;
+    if (!g.ws.io_pin || !g.ws.x_io || !g.ws.out_io)
+        return fail(HFMOE_ERR_NOT_INITIALIZED, "host-contract buffers are not allocated");
     float* pin = g.ws.io_pin;
     float* pin_dev = g.ws.io_pin_dev;
     memcpy(pin, input_host, bytes);

@@ -136,6 +136,12 @@ int hfmoe_register_dense_layer(int layer, const hfmoe_dense_weights* w) {
     if (rc) return rc;
     if (!w || !w->gate_dev || !w->up_dev || !w->down_dev)
         return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d: dense gate, up and down weights are required", layer);
+    // 16-byte vector and LDS-DMA loads read the three matrices; the norm weight is read per element.
+    rc = check_align(layer, "dense gate", w->gate_dev, 16);
+    if (!rc) rc = check_align(layer, "dense up", w->up_dev, 16);
+    if (!rc) rc = check_align(layer, "dense down", w->down_dev, 16);
+    if (!rc) rc = check_align(layer, "post_attention_norm", w->post_attention_norm_dev, 2);
+    if (rc) return rc;
     const int inter = w->intermediate;
     const int slice = inter > 0 && inter % 8 == 0 ? dense_slice(inter) : 0;
     if (!slice)

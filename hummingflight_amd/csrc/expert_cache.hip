@@ -136,6 +136,17 @@ struct ExpertCache {
         return victim;
     }
 
+    // Unmap a slot whose upload could not be queued: its bytes are the evicted
+    // expert's, so a later stage of the key must copy again and an FFN call
+    // must report the expert as not resident.
+    void forget(int slot) {
+        DevExpert& d = experts[slot];
+        if (d.key != ~0ull) where.erase(d.key);
+        d.key = ~0ull;
+        d.last_use = 0;
+        d.pending = false;
+    }
+
     // Round-robin staging slot; a slot whose copy is still queued is drained
     // first so its host bytes are never overwritten in flight
     // (cuda_backend.cpp:302-312).
@@ -219,14 +230,23 @@ int hfmoe_expert_stage(int layer, int expert_id, const uint16_t* w, int hidden, 
     const int slot = c.acquire(ExpertCache::key_of(layer, expert_id), need);
     if (!need) return HFMOE_OK;
     const int st = c.claim_stage();
-    if (st < 0) return fail(HFMOE_ERR_HIP, "staging slot drain failed");
+    if (st < 0) {
+        c.forget(slot);
+        return fail(HFMOE_ERR_HIP, "staging slot drain failed");
+    }
     const size_t bytes = c.expert_bytes();
     staging_memcpy(c.stage_host[st], w, bytes);
     hipError_t e = hipMemcpyAsync(c.experts[slot].w, c.stage_host[st], bytes, hipMemcpyHostToDevice,
                                   g.copy_stream);
     if (e == hipSuccess) e = hipEventRecord(c.stage_done[st], g.copy_stream);
     if (e == hipSuccess) e = hipEventRecord(c.experts[slot].uploaded, g.copy_stream);
-    if (e != hipSuccess) return fail_hip(e, "expert upload");
+    if (e != hipSuccess) {
+        // The copy may be queued with its events unrecorded: drain it before
+        // the staging slot or the HBM slot is reused.
+        (void)hipStreamSynchronize(g.copy_stream);
+        c.forget(slot);
+        return fail_hip(e, "expert upload");
+    }
     c.stage_busy[st] = 1;
     c.experts[slot].pending = true;
     c.experts[slot].stage_slot = st;

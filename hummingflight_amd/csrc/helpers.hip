@@ -14,6 +14,7 @@
 // embedding widens BF16 to FP32 exactly; softmax is exp(x - max) scaled by one
 // reciprocal of the sum; argmax keeps the first largest element.
 #include "hf_api_internal.h"
+#include "hf_expf.h"
 
 #include <climits>
 
@@ -31,6 +32,13 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t* __restri
     float* o = out + (size_t)t * hidden;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
         o[i] = ok ? __uint_as_float((uint32_t)row[i] << 16) : 0.0f;
+}
+
+// y[i] = sigmoid_f32(x[i]) (moe_router.h:19-21), the router's scoring function.
+__global__ __launch_bounds__(256) void router_sigmoid_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = router_sigmoid(x[i]);
 }
 
 constexpr int kSoftmaxThreads = 1024;
@@ -146,6 +154,18 @@ int hfmoe_softmax_rows(float* x_dev, int32_t T, int32_t n, void* stream) {
     if (T == 0) return HFMOE_OK;
     hipError_t e = launch(softmax_rows_kernel, dim3(T), dim3(kSoftmaxThreads), 0, pick_stream(stream), x_dev, n);
     return e == hipSuccess ? HFMOE_OK : fail_hip(e, "softmax launch");
+}
+
+int hfmoe_router_sigmoid(const float* x_dev, float* y_dev, int64_t n, void* stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (n < 0 || (n > 0 && (!x_dev || !y_dev)))
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "router sigmoid: null buffer or n < 0");
+    if (n == 0) return HFMOE_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+    hipError_t e = launch(router_sigmoid_kernel, dim3((unsigned)blocks), dim3(256), 0, pick_stream(stream), x_dev,
+                          y_dev, n);
+    return e == hipSuccess ? HFMOE_OK : fail_hip(e, "router sigmoid launch");
 }
 
 int hfmoe_argmax_rows(const float* x_dev, int32_t T, int32_t n, int32_t* best_dev, void* stream) {

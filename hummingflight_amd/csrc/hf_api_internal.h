@@ -144,6 +144,8 @@ int fail_hip(hipError_t e, const char* what);
 int require_init();
 int require_cfg();
 int env_int(const char* name, int dflt);
+// HFMOE_ERR_INVALID_ARGUMENT naming the layer and tensor when p % align != 0.
+int check_align(int layer, const char* what, const void* p, size_t align);
 hipStream_t pick_stream(void* s);
 void prof_begin(Pending& p, const char* name, hipStream_t s);
 void prof_end(Pending& p, hipStream_t s);

@@ -21,6 +21,10 @@ extern LaunchTiming g_timing;
 template <typename... Params>
 inline hipError_t launch_exact(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem,
                                hipStream_t s, Params... args) {
+    // The launch reports through the thread's last-error slot: clear what an
+    // earlier call left there (a refused allocation, say) so it is not taken
+    // for this launch's failure.
+    (void)hipGetLastError();
     if (g_timing.stop) {
         hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, g_timing.start, g_timing.stop, 0u, args...);
         g_timing.start = nullptr;
@@ -40,6 +44,9 @@ inline hipError_t launch(void (*kernel)(Params...), dim3 grid, dim3 block, uint3
 }
 
 constexpr int kRouterTokTile = 8;   // tokens per pass of the multi-token router GEMV
+// Largest max_tokens of a configuration: keeps every [rows, hidden] index of
+// the multi-token path (rows = T * (k + n_shared) <= 131072) below 2^31.
+constexpr int kMaxTokens = 8192;
 constexpr int kMaxSlots = 16;       // routed + shared slices handled by the T=1 GEMVs
 constexpr int kDownMaxRows = 64;    // output rows per block of the decode down projection
 

@@ -18,12 +18,13 @@
 // wave-wide reductions.
 //
 // Every floating-point step is a single IEEE operation written out in this
-// file with contraction off, so given the same logits the selection and the
-// weights follow the reference's operation order exactly; exp is evaluated in
-// double and rounded once (correctly rounded expf).
+// file with contraction off, and the sigmoid is glibc's expf algorithm
+// (hf_expf.h), so given the same logits the selection and the weights are the
+// reference's bit for bit.
 #pragma once
 
 #include "hf_common.h"
+#include "hf_expf.h"
 
 namespace hf {
 
@@ -32,18 +33,12 @@ constexpr int kSelectPerThread = kMaxExperts / kSelectThreads;
 constexpr int kSelectChunk = 32;    // preferred chunk size for stage A
 constexpr int kSelectMaxChunks = 64;
 
-__device__ __forceinline__ float sigmoid_cr(float x) {
-#pragma clang fp contract(off)
-    const float e = (float)exp(-(double)x);
-    return 1.0f / (1.0f + e);
-}
-
 // Score pair of one expert, written by the router kernels next to its logit:
 // s = sigmoid(logit) (glm_forward.cpp:522-524) and key = s + bias
 // (moe_router.h:38-41), the value experts are ranked on.
 __device__ __forceinline__ float2 score_pair(float logit, const float* bias, int e) {
 #pragma clang fp contract(off)
-    const float s = sigmoid_cr(logit);
+    const float s = router_sigmoid(logit);
     return make_float2(s, bias ? s + bias[e] : s);
 }
 

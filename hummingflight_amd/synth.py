@@ -64,6 +64,9 @@ class DeviceLayer:
     every expert still has its own address range in the table only if
     distinct_experts >= n_experts).
     bias: optional explicit F32 [E] correction bias (else ~N(0, bias_std)).
+    register_as: layer id to register under (default `layer`, which seeds the
+    tensors), so one weight set can be registered twice, e.g. streamed and
+    HBM-resident.
     """
     shape: LayerShape
     layer: int = 0
@@ -74,6 +77,7 @@ class DeviceLayer:
     experts_on_host: bool = False
     distinct_experts: int | None = None
     with_norm: bool = False
+    register_as: int | None = None
     buffers: list = field(default_factory=list, repr=False)
 
     def __post_init__(self):
@@ -129,7 +133,8 @@ class DeviceLayer:
                               C.cast(ptrs, C.c_void_p),
                               self.norm.ptr if self.norm else None,
                               capi.EXPERTS_HOST_PINNED if self.experts_on_host else capi.EXPERTS_DEVICE, 0)
-        capi.call("hfmoe_register_layer", self.layer, C.byref(w))
+        self.layer_id = self.layer if self.register_as is None else self.register_as
+        capi.call("hfmoe_register_layer", self.layer_id, C.byref(w))
 
     def _dev(self, nbytes: int) -> capi.DeviceBuffer:
         b = capi.DeviceBuffer(nbytes)

@@ -64,12 +64,17 @@ typedef struct hfmoe_config {
     uint64_t vram_budget_bytes;   /* AdaptiveConfig::vramBudgetBytes
                                      (src/runtime/runtime_config.h:62); bounds the
                                      streamed-expert staging pool; 0 = default */
-    int32_t max_tokens;           /* largest T of one forward call (workspace) */
+    int32_t max_tokens;           /* largest T of one forward call (workspace), <= 8192 */
     int32_t reserved;
 } hfmoe_config;
 
 /* One MoE layer's tensors (LayerWeights / ExpertWeights,
  * src/model/weight_index.h:28-36,58-67).  BF16 values are raw uint16 bits. */
+/* Alignment: BF16 matrices read from HBM (router, shared expert, routed
+ * experts with HFMOE_EXPERTS_DEVICE) must be 16-byte aligned, the bias 4-byte
+ * and the norm weight 2-byte; hfmoe_register_layer returns
+ * HFMOE_ERR_INVALID_ARGUMENT otherwise.  Host-pinned experts may sit at any
+ * address (the DMA engines copy them into the library's aligned slots). */
 typedef struct hfmoe_layer_weights {
     const uint16_t* router_dev;       /* mlp.gate.weight      [E, hidden] */
     const float* score_bias_dev;      /* e_score_correction_bias F32 [E], or NULL */
@@ -127,6 +132,7 @@ typedef struct hfmoe_dense_weights {
     int32_t intermediate;      /* intermediateSize (config.h:16) */
     int32_t reserved;
 } hfmoe_dense_weights;
+/* The three matrices must be 16-byte aligned, the norm weight 2-byte. */
 int hfmoe_register_dense_layer(int layer, const hfmoe_dense_weights* w);
 /* out_dev[T, hidden] = Wd.(silu(Wg.x) * (Wu.x)), FP32 in and out. */
 int hfmoe_dense_mlp_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
@@ -156,6 +162,10 @@ int hfmoe_embedding_gather(const uint16_t* emb_dev, int token_id, float* out_dev
 int hfmoe_matvec_bf16_dev(const uint16_t* w_dev, const float* x_dev, float* y_dev, int M, int K, void* stream);
 int hfmoe_softmax_rows(float* x_dev, int32_t T, int32_t n, void* stream);
 int hfmoe_argmax_rows(const float* x_dev, int32_t T, int32_t n, int32_t* best_dev, void* stream);
+/* y_dev[i] = 1 / (1 + expf(-x_dev[i])) in float, i < n: the router's scoring
+ * function (sigmoid_f32, moe_router.h:19-21), bit-identical to the reference's
+ * (glibc's expf) for every float input. */
+int hfmoe_router_sigmoid(const float* x_dev, float* y_dev, int64_t n, void* stream);
 
 /* ---- per-expert plugin surface (cuda_backend.h:64-90) ---- */
 int hfmoe_expert_cache_config(int capacity, int staging_depth); /* gpuExpertCacheConfig */

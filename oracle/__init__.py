@@ -71,6 +71,7 @@ def lib() -> C.CDLL:
         L.orc_gemv_bf16_f32_avx2.argtypes = L.orc_gemv_bf16_f32.argtypes
         L.orc_sigmoid.restype = C.c_float
         L.orc_sigmoid.argtypes = [C.c_float]
+        L.orc_sigmoid_n.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         L.orc_topk_flat.restype = C.c_int
         L.orc_topk_flat.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_float, C.c_int,
                                     C.c_void_p, C.c_void_p]
@@ -177,6 +178,14 @@ def gemv(A: np.ndarray, x: np.ndarray, alpha=1.0, beta=0.0, y=None, avx2=False) 
     rc = fn(_p(A), _p(x), _p(y), M, K, alpha, beta)
     if avx2 and rc != 0:
         raise RuntimeError("AVX2 restatement not built")
+    return y
+
+
+def sigmoid(x: np.ndarray) -> np.ndarray:
+    """1/(1 + expf(-x)) per element in float (moe_router.h:19-21), glibc expf."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_sigmoid_n(_p(x), _p(y), x.size)
     return y
 
 

@@ -46,6 +46,11 @@ void orc_gemv_bf16_f32(const uint16_t* A, const float* x, float* y,
  * library's single-precision exp (std::exp(float) is expf). */
 float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+/* orc_sigmoid over an array (the GPU tests compare millions of inputs). */
+void orc_sigmoid_n(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_sigmoid(x[i]);
+}
+
 /* Strict "a ranks before b": larger value first, then lower index. */
 static int ranks_before(float va, int ia, float vb, int ib) {
     if (va > vb) return 1;

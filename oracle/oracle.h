@@ -43,6 +43,7 @@ int orc_gemv_bf16_f32_avx2(const uint16_t* A, const float* x, float* y,
 
 /* ---- sigmoid (src/compute/moe_router.h:19-21, glm_forward.cpp:522-524) ---- */
 float orc_sigmoid(float x);
+void orc_sigmoid_n(const float* x, float* y, int64_t n);
 
 /* ---- flat noaux_tc top-k (src/compute/moe_router.h:29-57) ----
  * Ranks experts on scores[i]+bias[i] (bias may be NULL), keeps k (<= 8) in

@@ -1,7 +1,9 @@
 """Shared GPU-test harness: a configured layer on the device and its oracle twin.
 
-Bar: expert indices bit-exact given the same router logits; outputs within
-1e-2 relative + 2e-3 absolute of the oracle (BF16 weights, FP32 accumulation).
+Bar: expert indices and routing weights bit-exact given the same router
+logits (the device sigmoid is glibc's expf algorithm, tests/test_expf.py);
+outputs within 1e-2 relative + 2e-3 absolute of the oracle (BF16 weights,
+FP32 accumulation).
 """
 import ctypes as C
 
@@ -76,7 +78,7 @@ class Run:
         """Selection given the GPU's logits, then the output given that selection."""
         ridx, rw = self.ref.route(res["logits"][t])
         assert res["idx"][t].tolist() == ridx.tolist(), f"token {t}: selection differs"
-        assert ulp_diff(res["w"][t], rw).max() <= 2, f"token {t}: weights differ"
+        assert ulp_diff(res["w"][t], rw).max() == 0, f"token {t}: weights differ"
         ref = self.ref.combine(x, ridx, rw)
         assert_close(res["out"][t], ref, f"token {t} output")
         return ridx, ref

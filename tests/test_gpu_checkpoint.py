@@ -70,7 +70,7 @@ def check(ref, x, res):
     for t in range(x.shape[0]):
         ridx, rw = ref.route(lg[t])
         assert idx[t].tolist() == ridx.tolist(), f"token {t}: selection"
-        assert ulp_diff(w[t], rw).max() <= 2
+        assert ulp_diff(w[t], rw).max() == 0
         assert_close(out[t], ref.combine(x[t], ridx, rw), f"token {t}")
 
 

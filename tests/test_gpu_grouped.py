@@ -306,3 +306,28 @@ def test_grouped_edge_shapes(hf, name, dims, routing, n_group, topk_group, n_sha
     check_vs_decode(r, x, res, range(0, T, max(1, T // 4)), dims["hidden"])
     x.free()
     r.free()
+
+
+def test_batched_decode_t64_zipf(hf):
+    # Batched decode at full shape: 64 tokens, correction bias calibrated for
+    # Zipf(1.1) expert popularity (tests/golden/zipf_bias_e256.json), the
+    # benchmark's own layer and tokens.  The hottest expert carries most of the
+    # 64 rows beside ~130 experts with one or two rows, so the 128-row grouped
+    # GEMM runs every per-wavefront row-block count (2, 1 and 0 of its 32-row
+    # slices in use).  Every token against the oracle.
+    with open(os.path.join(os.path.dirname(__file__), "golden", "zipf_bias_e256.json")) as fh:
+        zb = json.load(fh)
+    T, d, E = 64, FULL["hidden"], FULL["n_experts"]
+    seed = zb["layer_seed"]
+    r = Run(FULL, n_group=8, topk_group=4, seed=seed, T=T, bias=np.array(zb["bias"], np.float32))
+    x = synth.make_x_dev(T, d, seed=seed)
+    res = r.forward(x, T)
+    counts = check_dispatch(res, E)
+    U = int((counts > 0).sum())
+    print(f"T=64 Zipf: {U} distinct experts, hottest {int(counts.max())} rows", flush=True)
+    assert counts.max() > 32 and U > 100 and (counts == 1).sum() > 32
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    for t in range(T):
+        r.check_token(xh[t], res, t)
+    x.free()
+    r.free()

@@ -130,3 +130,27 @@ def test_helpers_reject_bad_arguments(configured):
     assert lib.hfmoe_argmax(None, 4, None) == capi.ERR_INVALID_ARGUMENT
     assert lib.hfmoe_embedding_lookup(None, 0, ptr(x), 4) == capi.ERR_INVALID_ARGUMENT
     assert lib.hfmoe_matvec_bf16(ptr(x), ptr(x), ptr(x), 0, 4) == capi.ERR_INVALID_ARGUMENT
+
+
+def test_router_sigmoid_matches_the_c_library(hf):
+    # The router's sigmoid on the device against 1/(1 + expf(-x)) with glibc's
+    # expf (the oracle), bit for bit: every 256th float bit pattern (each
+    # exponent, both signs, with the low byte varied), and every 97th float of
+    # either sign below 16 in magnitude, where router logits live.
+    i = np.arange(1 << 24, dtype=np.uint64)
+    sweep = ((i << np.uint64(8)) | ((i * np.uint64(37)) & np.uint64(255))).astype(np.uint32)
+    pos = np.arange(0, 0x41800000, 97, dtype=np.uint32)
+    dense = np.concatenate([pos, pos | np.uint32(0x80000000)])
+    for bits in (sweep, dense):
+        x = bits.view(np.float32)
+        x = x[~np.isnan(x)]
+        xb = capi.DeviceBuffer.of(x)
+        yb = capi.DeviceBuffer(x.size * 4)
+        capi.call("hfmoe_router_sigmoid", xb.ptr, yb.ptr, x.size, None)
+        capi.call("hfmoe_synchronize")
+        got = yb.download(np.float32, x.size)
+        ref = O.sigmoid(x)
+        bad = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+        assert bad.size == 0, f"{bad.size} differ, first x={x[bad[0]]!r}: {got[bad[0]]!r} vs {ref[bad[0]]!r}"
+        xb.free()
+        yb.free()

@@ -4,6 +4,8 @@ Bar: expert indices bit-exact given the same router logits; outputs within
 1e-2 relative + 2e-3 absolute of the oracle, which is itself bit-exact with
 the reference's moeLayer (test_oracle.py).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -94,13 +96,93 @@ def test_decode_is_deterministic(hf):
 
 
 def test_host_contract_moe_layer(hf):
-    # hfmoe_moe_layer: host float[hidden] in and out, as GLMForward::moeLayer.
+    # hfmoe_moe_layer: host float[hidden] in and out, as GLMForward::moeLayer;
+    # two calls with different tokens through the same pinned io buffer.
     r = Run(SMALL, seed=13)
-    xh = O.make_x(1, SMALL["hidden"], 13)[0].copy()
+    xs = O.make_x(2, SMALL["hidden"], 13)
+    for t in range(2):
+        xh = xs[t].copy()
+        out = np.zeros(SMALL["hidden"], np.float32)
+        capi.call("hfmoe_moe_layer", 0, xh.ctypes.data, out.ctypes.data)
+        ref, lg, idx, w = r.ref.forward(xh)
+        assert_close(out, ref, f"host contract token {t}")
+    r.free()
+
+
+def layer_weights(dev, **override):
+    """hfmoe_layer_weights of a synth.DeviceLayer, fields replaced by `override`."""
+    f = dict(router=dev.router.ptr, bias=dev.bias_buf.ptr, sg=dev.shared[0].ptr, su=dev.shared[1].ptr,
+             sd=dev.shared[2].ptr, experts=C.cast(dev._ptrs, C.c_void_p), norm=None, loc=capi.EXPERTS_DEVICE)
+    f.update(override)
+    return capi.LayerWeights(f["router"], f["bias"], f["sg"], f["su"], f["sd"], f["experts"], f["norm"], f["loc"], 0)
+
+
+def test_misaligned_weights_are_rejected(hf):
+    # 16-byte vector and LDS-DMA loads read the weights: an 8-byte-aligned view
+    # (a safetensors tensor may start at any multiple of 8) is refused at
+    # registration, before anything is launched.
+    r = Run(SMALL, seed=3)
+    L = capi.load()
+    capi.call("hfmoe_profile_enable", 1)
+    capi.call("hfmoe_profile_reset")
+    dev = r.dev
+    cases = [dict(router=dev.router.ptr + 8), dict(sg=dev.shared[0].ptr + 8), dict(sd=dev.shared[2].ptr + 8),
+             dict(bias=dev.bias_buf.ptr + 2), dict(norm=dev.router.ptr + 1)]
+    for case in cases:
+        w = layer_weights(dev, **case)
+        assert L.hfmoe_register_layer(5, C.byref(w)) == capi.ERR_INVALID_ARGUMENT, case
+        assert b"aligned" in L.hfmoe_last_error()
+    ptrs = (C.c_void_p * len(dev._ptrs))(*dev._ptrs)
+    ptrs[3 * 7 + 2] = ptrs[3 * 7 + 2] + 8
+    w = layer_weights(dev, experts=C.cast(ptrs, C.c_void_p))
+    assert L.hfmoe_register_layer(5, C.byref(w)) == capi.ERR_INVALID_ARGUMENT
+    assert b"expert 7 down" in L.hfmoe_last_error()
+    dw = capi.DenseWeights(dev.shared[0].ptr + 8, dev.shared[1].ptr, dev.shared[2].ptr, None, SMALL["inter"], 0)
+    assert L.hfmoe_register_dense_layer(6, C.byref(dw)) == capi.ERR_INVALID_ARGUMENT
+    # Nothing registered, nothing launched; the aligned table still registers.
+    x = synth.make_x_dev(1, SMALL["hidden"], seed=3)
+    out = capi.DeviceBuffer(SMALL["hidden"] * 4)
+    assert L.hfmoe_moe_forward(5, x.ptr, 1, out.ptr, None) == capi.ERR_NOT_REGISTERED
+    n = C.c_int(0)
+    capi.call("hfmoe_profile_read", None, 0, C.byref(n))
+    assert n.value == 0
+    capi.call("hfmoe_register_layer", 5, C.byref(layer_weights(dev)))
+    capi.call("hfmoe_profile_enable", 0)
+    x.free()
+    out.free()
+    r.free()
+
+
+def test_failed_configure_leaves_library_unconfigured(hf):
+    # A configuration whose workspace cannot be allocated (HBM filled from the
+    # host first) must not leave the previous one half in force.
+    L = capi.load()
+    r = Run(SMALL, seed=4)
+    held = []
+    for chunk in (16 << 30, 1 << 30, 64 << 20):
+        while True:
+            p = C.c_void_p()
+            if L.hfmoe_malloc(C.byref(p), chunk) != capi.OK:
+                break
+            held.append(p.value)
+    big = synth.LayerShape(hidden=8192, inter=4096, n_experts=256, top_k=8, n_group=8, topk_group=4)
+    rc = L.hfmoe_configure(C.byref(big.config(max_tokens=8192)))
+    for p in held:
+        capi.call("hfmoe_free", p)
+    assert rc == capi.ERR_OUT_OF_MEMORY, L.hfmoe_last_error()
+    xh = O.make_x(1, SMALL["hidden"], 4)[0].copy()
     out = np.zeros(SMALL["hidden"], np.float32)
+    assert L.hfmoe_moe_layer(0, xh.ctypes.data, out.ctypes.data) == capi.ERR_NOT_INITIALIZED
+    w = layer_weights(r.dev)
+    assert L.hfmoe_register_layer(0, C.byref(w)) == capi.ERR_NOT_INITIALIZED
+    assert L.hfmoe_moe_forward(0, None, 1, None, None) == capi.ERR_NOT_INITIALIZED
+    # Out-of-range max_tokens is refused before anything is released.
+    capi.call("hfmoe_configure", r.shape.config(max_tokens=1))
+    capi.call("hfmoe_register_layer", 0, C.byref(w))
+    assert L.hfmoe_configure(C.byref(r.shape.config(max_tokens=8193))) == capi.ERR_UNSUPPORTED
     capi.call("hfmoe_moe_layer", 0, xh.ctypes.data, out.ctypes.data)
-    ref, lg, idx, w = r.ref.forward(xh)
-    assert_close(out, ref, "host contract")
+    ref, _, _, _ = r.ref.forward(xh)
+    assert_close(out, ref, "after a refused configure")
     r.free()
 
 

@@ -101,7 +101,7 @@ def test_streamed_cache_and_copy_ahead(hf, opts):
         x = xs[i // LAYERS]
         ridx, rw = ref.route(r["logits"])
         assert r["idx"] == ridx.tolist(), f"token {i // LAYERS} layer {r['layer']}: selection"
-        assert ulp_diff(r["w"], rw).max() <= 2
+        assert ulp_diff(r["w"], rw).max() == 0
         assert_close(r["out"], ref.combine(x, ridx, rw), f"token {i // LAYERS} layer {r['layer']}")
 
     # Copy-ahead off, cache emptied: the same bits.
