@@ -192,6 +192,8 @@ int hfmoe_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(HFMOE_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
+    int rc = noalloc_setup(device);
+    if (rc) return rc;
     g.device = device;
     g.num_cus = prop.multiProcessorCount;
     g.total_mem = prop.totalGlobalMem;

@@ -35,34 +35,45 @@ int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s) {
     return e == hipSuccess ? HFMOE_OK : fail_hip(e, "debug copies");
 }
 
-int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg) {
+int forward_t1_on(LayerState& L, const float* x, float* out, hipStream_t s, const T1Buffers& b, bool profile) {
     const Cfg& c = g.cfg;
     const int nslots = c.k + c.n_shared;
     Pending p;
-    prof_begin(p, "router", s);
-    hipError_t e = launch_router_logits_t1(x, L.dev, c, g.ws.logits, g.ws.scores, s);
-    prof_end(p, s);
+    auto begin = [&](const char* name) {
+        if (profile) prof_begin(p, name, s);
+    };
+    auto end = [&]() {
+        if (profile) prof_end(p, s);
+    };
+    begin("router");
+    hipError_t e = launch_router_logits_t1(x, L.dev, c, b.logits, b.scores, s);
+    end();
     if (e != hipSuccess) return fail_hip(e, "router launch");
     // The gate/up kernel routes in place, overlapped with the loads of the
     // shared expert's first rows (HFMOE_FUSE_SELECT=0 runs selection as its own
     // kernel first, for comparison).
     const bool fused = env_int("HFMOE_FUSE_SELECT", 1) != 0;
     if (!fused) {
-        prof_begin(p, "select", s);
-        e = launch_select(g.ws.scores, 1, c, g.ws.idx, g.ws.wts, s);
-        prof_end(p, s);
+        begin("select");
+        e = launch_select(b.scores, 1, c, b.idx, b.wts, s);
+        end();
         if (e != hipSuccess) return fail_hip(e, "select launch");
     }
-    prof_begin(p, "expert_gateup", s);
-    e = launch_gateup_t1(x, L.dev, c, fused ? g.ws.scores : nullptr, g.ws.idx, g.ws.wts, g.ws.h,
-                         nslots, gu_blocks(), s);
-    prof_end(p, s);
+    begin("expert_gateup");
+    e = launch_gateup_t1(x, L.dev, c, fused ? b.scores : nullptr, b.idx, b.wts, b.h, nslots, gu_blocks(), s);
+    end();
     if (e != hipSuccess) return fail_hip(e, "gate/up launch");
-    prof_begin(p, "expert_down", s);
-    e = launch_down_t1(g.ws.h, L.dev, c, g.ws.idx, g.ws.wts, nullptr, out, nslots, dn_blocks(), s);
-    prof_end(p, s);
+    begin("expert_down");
+    e = launch_down_t1(b.h, L.dev, c, b.idx, b.wts, nullptr, out, nslots, dn_blocks(), s);
+    end();
     if (e != hipSuccess) return fail_hip(e, "down launch");
-    return copy_debug(dbg, 1, s);
+    return HFMOE_OK;
+}
+
+int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg) {
+    const T1Buffers b{g.ws.logits, g.ws.scores, g.ws.idx, g.ws.wts, g.ws.h};
+    int rc = forward_t1_on(L, x, out, s, b, true);
+    return rc ? rc : copy_debug(dbg, 1, s);
 }
 
 }  // namespace hf

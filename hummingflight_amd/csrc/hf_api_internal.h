@@ -151,10 +151,26 @@ void prof_begin(Pending& p, const char* name, hipStream_t s);
 void prof_end(Pending& p, hipStream_t s);
 void prof_drain();
 
+// Scratch of the T = 1 decode kernels: router logits [E], score pairs [E],
+// selected ids [k], routing weights [k], h [k + n_shared, I].
+struct T1Buffers {
+    float* logits;
+    float2* scores;
+    int* idx;
+    float* wts;
+    float* h;
+};
+
 // forward.hip
 int gu_blocks();
 int dn_blocks();
 int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const hfmoe_route_debug* dbg);
+// The decode launches over explicit scratch; profile = false records no timing
+// events (so the call creates none).
+int forward_t1_on(LayerState& L, const float* x, float* out, hipStream_t s, const T1Buffers& b, bool profile);
+// noalloc.hip: the device address of this device's static scratch array
+// (hipGetSymbolAddress, once per device; called by hfmoe_init).
+int noalloc_setup(int device);
 int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                       const hfmoe_route_debug* dbg);
 int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s);

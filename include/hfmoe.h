@@ -115,6 +115,14 @@ int hfmoe_register_layer(int layer, const hfmoe_layer_weights* w);
 int hfmoe_moe_forward(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
 int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out_dev,
                             void* stream, const hfmoe_route_debug* dbg);
+/* hfmoe_moe_forward for one token (T <= 1) that allocates nothing: no
+ * counterpart in the reference; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Its scratch (router logits, score pairs, selection, h) lives in
+ * a 192 KiB static device array per GPU, held until the process ends; every
+ * shape hfmoe_configure accepts fits.  HBM-resident MoE layers only.  Calls on
+ * one GPU share that array: calls that overlap in time on one GPU race. */
+int hfmoe_moe_forward_noalloc(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
 /* The moeLayer contract itself: one token, host FP32 buffers, synchronous. */
 int hfmoe_moe_layer(int layer, const float* input_host, float* output_host);
 /* h_dev[T, hidden] += MLP(RMSNorm(h_dev)) -- the MLP half of a decoder layer
