@@ -34,6 +34,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -63,45 +64,108 @@ def algorithmic_bytes_t1(shape: synth.LayerShape) -> dict[str, int]:
             "layer": ns * 3 * I * d * 2 + E * d * 2 + E * 4 + d * 4 + d * 4}
 
 
+def host_cpu() -> dict:
+    """CPU model, sockets and cores of this host (lscpu), and the CPU share the bench uses."""
+    info = {"model": None, "sockets": None, "cores_per_socket": None, "threads_per_core": None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "Model name":
+                info["model"] = val
+            elif key == "Socket(s)":
+                info["sockets"] = int(val)
+            elif key == "Core(s) per socket":
+                info["cores_per_socket"] = int(val)
+            elif key == "Thread(s) per core":
+                info["threads_per_core"] = int(val)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if info["sockets"] and info["cores_per_socket"]:
+        info["physical_cores"] = info["sockets"] * info["cores_per_socket"]
+    info["logical_cpus"] = os.cpu_count()
+    try:
+        info["cpus_allowed"] = len(os.sched_getaffinity(0))
+    except OSError:
+        info["cpus_allowed"] = None
+    return info
+
+
+def set_omp_threads(n: int) -> None:
+    """Thread count of the OpenMP parallel regions started from this thread (both CPU libraries)."""
+    C.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+
+
 def cpu_baseline_decode(shape: synth.LayerShape, seed: int, seconds: float) -> dict:
-    """The reference's own moeLayer (oracle/_ref) on this host, else the C restatement."""
+    """The reference CPU MoE layer on this host, T = 1, full shape, weights in host RAM.
+
+    `value`: the reference's own moeLayer (oracle/_ref, compiled from its
+    sources with its Linux flags: the scalar serial GEMV) on the host's CPU
+    share; beside it, `variants`: the same on one core, the restated MSVC
+    AVX2+FMA GEMV build (the one behind the reference's published numbers) on
+    the CPU share and on one core, and both builds with the scheduler's 72 MB
+    copy of every used expert (scheduler.cpp:646-660).  The restatement routes
+    with the GPU's 8-group rule; the reference routes flat (it has no group
+    rule): the same 8 + 1 experts of work either way.
+    """
     import oracle as O
-    spec = O.LayerSpec(hidden=shape.hidden, inter=shape.inter, n_experts=shape.n_experts,
-                       top_k=shape.top_k, n_group=1, topk_group=1, n_shared=shape.n_shared, seed=seed)
-    layer = O.SyntheticLayer(spec)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    spec_flat = O.LayerSpec(hidden=shape.hidden, inter=shape.inter, n_experts=shape.n_experts,
+                            top_k=shape.top_k, n_group=1, topk_group=1, n_shared=shape.n_shared, seed=seed)
+    spec_grp = O.LayerSpec(hidden=shape.hidden, inter=shape.inter, n_experts=shape.n_experts,
+                           top_k=shape.top_k, n_group=shape.n_group, topk_group=shape.topk_group,
+                           n_shared=shape.n_shared, seed=seed)
     x = O.make_x(1, shape.hidden, seed)[0].copy()
-    idx, _ = layer.route(layer.logits(x))  # the reference routes flat (no groups)
-    W, keep = layer.weights(idx)
     out = np.zeros(shape.hidden, np.float32)
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    flat, grp = O.SyntheticLayer(spec_flat), O.SyntheticLayer(spec_grp)
+    Wf, keep_f = flat.weights(flat.route(flat.logits(x))[0])
+    Wg, keep_g = grp.weights(grp.route(grp.logits(x))[0])
+    scratch = np.empty(3 * shape.hidden * shape.inter, np.uint16)
+
+    def sample(call) -> tuple[float, int]:
+        """(seconds per call, calls) of a bounded sample; `call(n)` runs n calls, returns seconds in all."""
+        first = call(1)  # warm: pages in the weights, sizes the sample
+        iters = max(2, min(500, int(seconds / max(first, 1e-6))))
+        return call(iters) / iters, iters
+
     R = O.ref()
-    if R is not None:
+
+    def ref_call(n: int) -> float:
         sec = C.c_double()
-        # One call to size the sample, then a bounded timed sample.
-        rc = R.ref_moe_layer_timed(b"/tmp/hfmoe_bench_ref_layer.bin", C.byref(spec.cfg()), C.byref(W),
-                                   x.ctypes.data, out.ctypes.data, 1, C.byref(sec))
+        rc = R.ref_moe_layer_timed(b"/tmp/hfmoe_bench_ref_layer.bin", C.byref(spec_flat.cfg()), C.byref(Wf),
+                                   x.ctypes.data, out.ctypes.data, n, C.byref(sec))
         if rc != 0:
             raise RuntimeError(f"reference harness failed rc={rc}")
-        iters = max(3, min(500, int(seconds / max(sec.value, 1e-6))))
-        rc = R.ref_moe_layer_timed(b"/tmp/hfmoe_bench_ref_layer.bin", C.byref(spec.cfg()), C.byref(W),
-                                   x.ctypes.data, out.ctypes.data, iters, C.byref(sec))
-        if rc != 0:
-            raise RuntimeError(f"reference harness failed rc={rc}")
-        kind, per_call = "reference", sec.value
-    else:
-        lib = O.lib()
-        t0 = time.perf_counter()
-        lib.orc_moe_layer(C.byref(spec.cfg()), C.byref(W), x.ctypes.data, out.ctypes.data, None, None, None)
-        first = time.perf_counter() - t0
-        iters = max(3, min(500, int(seconds / max(first, 1e-6))))
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            lib.orc_moe_layer(C.byref(spec.cfg()), C.byref(W), x.ctypes.data, out.ctypes.data, None, None, None)
-        kind, per_call = "port", (time.perf_counter() - t0) / iters
-    return {"value": 1.0 / per_call, "unit": "tokens/s", "cores": cores, "kind": kind,
-            "sample": f"{iters} moeLayer calls, T=1, d={shape.hidden}, {shape.n_experts} experts top-{shape.top_k} "
-                      f"+ {shape.n_shared} shared, flat routing, OpenMP threads={cores}; "
-                      f"{per_call * 1e3:.2f} ms/call"}
+        return sec.value * n  # the harness reports seconds per call
+
+    def port_call(avx2: int, copy: bool):
+        def call(n: int) -> float:
+            sec = O.lib().orc_moe_layer_bench(C.byref(spec_grp.cfg()), C.byref(Wg), x.ctypes.data,
+                                              out.ctypes.data, avx2, scratch.ctypes.data if copy else None, n)
+            if sec < 0:
+                raise RuntimeError("oracle bench failed")
+            return sec
+        return call
+
+    runs = []
+    for build, threads, copy in [("linux-scalar", share, False), ("linux-scalar", 1, False),
+                                 ("msvc-avx2-fma", share, False), ("msvc-avx2-fma", 1, False),
+                                 ("linux-scalar", share, True), ("msvc-avx2-fma", share, True)]:
+        use_ref = build == "linux-scalar" and not copy and R is not None
+        set_omp_threads(threads)
+        per_call, iters = sample(ref_call if use_ref else port_call(int(build != "linux-scalar"), copy))
+        runs.append({"kind": "reference" if use_ref else "port", "gemv": build, "threads": threads,
+                     "scheduler_copy": copy, "tokens_per_s": round(1.0 / per_call, 2),
+                     "ms_per_call": round(per_call * 1e3, 3), "calls": iters})
+    set_omp_threads(share)
+    head = runs[0]
+    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": share, "kind": head["kind"],
+            "sample": f"{head['calls']} moeLayer calls, T=1, d={shape.hidden}, {shape.n_experts} experts "
+                      f"top-{shape.top_k} + {shape.n_shared} shared, weights in host RAM, "
+                      f"{head['gemv']} GEMV, {share} OpenMP threads (the host's CPU share); "
+                      f"{head['ms_per_call']} ms/call",
+            "host": host_cpu(), "variants": runs}
 
 
 def time_steps(step, steps: int, warmup: int) -> float:
@@ -115,19 +179,49 @@ def time_steps(step, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) / steps
 
 
+def decode_routing(x_all, ntok: int, shape: synth.LayerShape) -> dict:
+    """Selections of the benchmark's tokens (one debug call each, untimed)."""
+    d, k, E = shape.hidden, shape.top_k, shape.n_experts
+    out, idx = capi.DeviceBuffer(d * 4), capi.DeviceBuffer(k * 4)
+    dbg = capi.RouteDebug(None, idx.ptr, None, None, None)
+    sel = []
+    for t in range(ntok):
+        capi.call("hfmoe_moe_forward_debug", 0, x_all.ptr + t * d * 4, 1, out.ptr, None, C.byref(dbg))
+        sel.append(set(idx.download(np.int32, k).tolist()))
+    out.free()
+    idx.free()
+    shared_prev = [len(sel[t] & sel[t - 1]) for t in range(ntok)]
+    return {"tokens_cycled": ntok, "distinct_selections": len({frozenset(s) for s in sel}),
+            "experts_hit": len(set().union(*sel)),
+            "routed_experts_shared_with_previous_step": round(float(np.mean(shared_prev)), 3)}
+
+
 def run_decode(args) -> dict:
+    """T = 1 decode, one MoE layer; each step takes the next of 64 distinct tokens
+    (different routing every step, as real decode), cycling."""
     shape = synth.LayerShape(**FULL)
     capi.call("hfmoe_configure", shape.config(max_tokens=1))
     layer = synth.DeviceLayer(shape, layer=0, seed=args.seed, experts_on_host=False)
-    x = synth.make_x_dev(1, shape.hidden, seed=args.seed)
+    ntok = 64
+    x_all = synth.make_x_dev(ntok, shape.hidden, seed=args.seed)
+    x = capi.DeviceBuffer.of(x_all.download(np.float32, shape.hidden))  # token 0 alone
     out = capi.DeviceBuffer(shape.hidden * 4)
     fwd = capi.load().hfmoe_moe_forward
+    routing = decode_routing(x_all, ntok, shape)
+    tok = [0]
 
     def step():
+        rc = fwd(0, x_all.ptr + (tok[0] % ntok) * shape.hidden * 4, 1, out.ptr, None)
+        tok[0] += 1
+        if rc:
+            capi.check(rc)
+
+    def same_step():
         rc = fwd(0, x.ptr, 1, out.ptr, None)
         if rc:
             capi.check(rc)
 
+    sec_same = None if args.decode_only else time_steps(same_step, args.steps, args.warmup)
     sec = time_steps(step, args.steps, args.warmup)
     # Same steps again, each kernel recording its own dispatch timestamps.
     prof, sec_prof = profiled_pass(step, args.steps)
@@ -143,7 +237,8 @@ def run_decode(args) -> dict:
     res = {
         "value": 1.0 / sec,
         "ms_per_step": sec * 1e3,
-        "config": {"workload": "moe_layer_decode", "tokens": 1, "hidden": shape.hidden,
+        "config": {"workload": "moe_layer_decode", "tokens": 1, "distinct_tokens_cycled": ntok,
+                   "hidden": shape.hidden,
                    "moe_intermediate": shape.inter, "routed_experts": shape.n_experts,
                    "shared_experts": shape.n_shared, "top_k": shape.top_k,
                    "n_group": shape.n_group, "topk_group": shape.topk_group,
@@ -155,7 +250,17 @@ def run_decode(args) -> dict:
                       "frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "ms_per_step_with_kernel_events": sec_prof * 1e3,
         "kernels": kernels,
+        "routing": routing,
     }
+    if sec_same is not None:
+        res["same_token_every_step"] = {"tokens_per_s": round(1.0 / sec_same, 1),
+                                        "us_per_step": round(sec_same * 1e6, 2),
+                                        "note": "one token replayed: its 9 experts re-read each step"}
+    if args.decode_only:
+        layer.free()
+        for b in (x, x_all, out):
+            b.free()
+        return res
     # The reference's host contract (moeLayer: host float[hidden] in and out,
     # synchronous), PCIe copies included; a note beside `value`, not `value`.
     xh = x.download(np.float32, shape.hidden).copy()
@@ -173,8 +278,8 @@ def run_decode(args) -> dict:
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_decode(shape, args.seed, args.cpu_seconds)
     layer.free()
-    x.free()
-    out.free()
+    for b in (x, x_all, out):
+        b.free()
     return res
 
 
@@ -494,7 +599,7 @@ def run_streamed(args, cached: bool = False) -> dict:
         cb = cpu_baseline_decode(shape, args.seed, args.cpu_seconds)
         cb["value"] /= n_layers
         cb["unit"] = "tokens/s"
-        cb["sample"] += f"; one layer timed, a token crosses {n_layers} layers"
+        cb["sample"] += f"; one layer timed, a token crosses {n_layers} layers (variants: per layer)"
         res["cpu_baseline"] = cb
     src.free()
     dst.free()
@@ -690,7 +795,10 @@ def main() -> int:
     ap.add_argument("--load-experts", type=int, default=64,
                     help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="decode: only the distinct-token steps (no same-token, host-contract or CPU legs), "
+                         "for kernel traces")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU baseline: seconds per variant")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "

@@ -72,6 +72,9 @@ def lib() -> C.CDLL:
         L.orc_sigmoid.restype = C.c_float
         L.orc_sigmoid.argtypes = [C.c_float]
         L.orc_sigmoid_n.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.orc_moe_layer_bench.restype = C.c_double
+        L.orc_moe_layer_bench.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                          C.c_int]
         L.orc_topk_flat.restype = C.c_int
         L.orc_topk_flat.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_float, C.c_int,
                                     C.c_void_p, C.c_void_p]

@@ -12,6 +12,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* dtype_bf16.h:19-24 -- zero-extend into the high half. */
 float orc_bf16_to_f32(uint16_t b) {
@@ -251,6 +252,78 @@ int orc_moe_combine(const orc_moe_cfg* cfg, const orc_moe_weights* W,
     }
     free(moe); free(eo); free(so); free(scratch);
     return rc;
+}
+
+/* ---- CPU-baseline form: the reference's two GEMV builds, optional
+ * scheduler copy, timed over `iters` calls ---- */
+typedef void (*orc_gemv_fn)(const uint16_t*, const float*, float*, int, int, float, float);
+
+static void gemv_avx2_void(const uint16_t* A, const float* x, float* y, int M, int K, float alpha, float beta) {
+    (void)orc_gemv_bf16_f32_avx2(A, x, y, M, K, alpha, beta);
+}
+
+/* orc_expert_ffn with the GEMV build as a parameter. */
+static void expert_ffn_g(orc_gemv_fn gemv, const uint16_t* Wg, const uint16_t* Wu, const uint16_t* Wd,
+                         const float* x, float* y, int hidden, int inter, float* scratch) {
+    float* g = scratch;
+    float* u = scratch + inter;
+    float* m = scratch + 2 * inter;
+    gemv(Wg, x, g, inter, hidden, 1.0f, 0.0f);
+    gemv(Wu, x, u, inter, hidden, 1.0f, 0.0f);
+    for (int i = 0; i < inter; ++i) m[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+    gemv(Wd, m, y, hidden, inter, 1.0f, 0.0f);
+}
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+double orc_moe_layer_bench(const orc_moe_cfg* cfg, const orc_moe_weights* W, const float* x, float* out,
+                           int avx2, void* copy_scratch, int iters) {
+    const int E = cfg->n_experts, H = cfg->hidden, I = cfg->inter;
+    const int Is = cfg->n_shared * I;
+    const int Imax = Is > I ? Is : I;
+    const size_t proj = (size_t)I * H;
+    orc_gemv_fn gemv = avx2 ? gemv_avx2_void : orc_gemv_bf16_f32;
+    float* lg = (float*)calloc((size_t)E, sizeof(float));
+    float* moe = (float*)calloc((size_t)H, sizeof(float));
+    float* eo = (float*)calloc((size_t)H, sizeof(float));
+    float* so = (float*)calloc((size_t)H, sizeof(float));
+    float* scratch = (float*)calloc((size_t)(3 * Imax), sizeof(float));
+    uint16_t* cp = (uint16_t*)copy_scratch;
+    double t0 = now_s(), t = -1.0;
+    for (int it = 0; it < iters; ++it) {
+        int sel[8];
+        float sw[8];
+        gemv(W->router, x, lg, E, H, 1.0f, 0.0f);
+        const int k = orc_route_from_logits(cfg, lg, W->bias, sel, sw);
+        for (int j = 0; j < H; ++j) moe[j] = 0.0f;
+        for (int r = 0; r < k; ++r) {
+            const int e = sel[r];
+            const uint16_t *g = W->expert_gate[e], *u = W->expert_up[e], *d = W->expert_down[e];
+            if (!g || !u || !d) goto done;
+            if (cp) { /* getExpertPtr: the resident expert copied into exScratch_ */
+                memcpy(cp, g, proj * 2);
+                memcpy(cp + proj, u, proj * 2);
+                memcpy(cp + 2 * proj, d, proj * 2);
+                g = cp;
+                u = cp + proj;
+                d = cp + 2 * proj;
+            }
+            expert_ffn_g(gemv, g, u, d, x, eo, H, I, scratch);
+            for (int j = 0; j < H; ++j) moe[j] += sw[r] * eo[j];
+        }
+        for (int j = 0; j < H; ++j) so[j] = 0.0f;
+        if (Is > 0 && W->shared_gate && W->shared_up && W->shared_down)
+            expert_ffn_g(gemv, W->shared_gate, W->shared_up, W->shared_down, x, so, H, Is, scratch);
+        for (int j = 0; j < H; ++j) out[j] = moe[j] + so[j];
+    }
+    t = now_s() - t0;
+done:
+    free(lg); free(moe); free(eo); free(so); free(scratch);
+    return t;
 }
 
 /* glm_forward.cpp:509-661 for one token. */

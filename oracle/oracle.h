@@ -136,6 +136,16 @@ int orc_moe_combine(const orc_moe_cfg* cfg, const orc_moe_weights* W,
                     const float* x, const int* idx, const float* w, int k,
                     float* out);
 
+/* The CPU baseline: `iters` moeLayer calls for one token, seconds in total
+ * (-1 when a selected expert has no weights).  avx2 = 0 runs the reference's
+ * Linux GEMV (scalar, serial, cpu_kernels.cpp:82-92), 1 its MSVC AVX2+FMA GEMV
+ * restated (:47-81).  copy_scratch (NULL, or >= 3*inter*hidden*2 bytes)
+ * receives each selected expert's [gate|up|down] by one memcpy before its
+ * FFN, as Scheduler::getExpertPtr copies a resident expert into its scratch
+ * (scheduler.cpp:646-660).  Threads: the OpenMP setting of the caller. */
+double orc_moe_layer_bench(const orc_moe_cfg* cfg, const orc_moe_weights* W, const float* x, float* out,
+                           int avx2, void* copy_scratch, int iters);
+
 /* ---- seeded counter-based generator (north-star extension) ----
  * Element i of tensor `tensor` under `seed`: three SplitMix64 outputs give
  * twelve 16-bit uniforms; z = (sum - 393210) / 65536 (exact, mean 0, var ~1,

@@ -6,6 +6,7 @@ reference's compiled sources), the reference's known-answer tests
 (src/self_test.cpp:53-200), and what the mathematics fixes (closed forms,
 brute force on tiny inputs, invariants).
 """
+import ctypes as C
 import itertools
 
 import numpy as np
@@ -439,3 +440,30 @@ def test_softmax_closed_forms(oracle_lib):
     assert np.allclose(O.softmax(x), O.softmax(xs), rtol=1e-5, atol=1e-8)
     y = O.softmax(np.array([0.0, 200.0, 0.0], np.float32))
     assert y[1] == 1.0 and y[0] == y[2] == 0.0  # exp(-200) underflows in FP32
+
+
+def test_cpu_baseline_bench_form(oracle_lib):
+    # orc_moe_layer_bench (the bench's CPU baseline) computes what orc_moe_layer
+    # computes: bit for bit with the Linux GEMV, with or without the scheduler's
+    # per-expert copy; within the AVX2 GEMV's reordering with the MSVC form.
+    O = oracle_lib
+    spec = O.LayerSpec(hidden=256, inter=128, n_experts=32, top_k=4, n_group=4, topk_group=2, seed=9)
+    L = O.SyntheticLayer(spec)
+    x = O.make_x(1, spec.hidden, 9)[0].copy()
+    ref, _, idx, _ = L.forward(x)
+    W, keep = L.weights(range(spec.n_experts))
+    cfg = spec.cfg()
+    scratch = np.zeros(3 * spec.hidden * spec.inter, np.uint16)
+    for avx2, copy in [(0, None), (0, scratch), (1, None), (1, scratch)]:
+        out = np.zeros(spec.hidden, np.float32)
+        sec = O.lib().orc_moe_layer_bench(C.byref(cfg), C.byref(W), x.ctypes.data, out.ctypes.data, avx2,
+                                          None if copy is None else copy.ctypes.data, 3)
+        assert sec > 0
+        if avx2:
+            assert np.max(np.abs(out - ref)) < 1e-3 * max(1.0, np.max(np.abs(ref)))
+        else:
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    # The copy path really computes from the copy: the last selected expert's bytes are in it.
+    e = int(idx[-1])
+    g, u, d = L.expert(e)
+    assert np.array_equal(scratch, np.concatenate([g, u, d]))
