@@ -13,6 +13,8 @@ Other workloads of the same layer:
   streamed  8 chained layers (RMSNorm + MoE + residual), T=1, routed experts in
             pinned host RAM, the selected ones copied to HBM on a side stream
   streamed_cached  the same with an HBM expert cache and next-layer copy-ahead
+  streamed_prefill one layer, T=4096, routed experts in pinned host RAM: the
+            batch's distinct experts cross PCIe a wave at a time
   dense     a dense-MLP layer (intermediate 12288), T=1 or --dense-tokens
   lm_head   final norm + LM head (vocab 154880) + greedy argmax, T=1
   load      a MoE layer from a safetensors shard into HBM (GB/s)
@@ -26,7 +28,7 @@ timestamps, recorded on the launch stream during a second pass of the timed
 steps), and the reference CPU path timed on this host as `cpu_baseline`.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload decode|batched|prefill|streamed|streamed_cached|dense|lm_head|load|plugin|copy]
+                    [--workload decode|batched|prefill|streamed|streamed_cached|streamed_prefill|dense|lm_head|load|plugin|copy]
 """
 from __future__ import annotations
 
@@ -524,6 +526,8 @@ def run_streamed(args, cached: bool = False) -> dict:
     opt = capi.StreamOptions()
     capi.call("hfmoe_stream_get_options", C.byref(opt))
     opt.overlap_floor = args.overlap_floor
+    opt.extra_depth = args.extra_depth
+    opt.prob_resident = int(args.prob_resident)
     capi.call("hfmoe_stream_set_options", C.byref(opt))
     layers = [synth.DeviceLayer(shape, layer=l, seed=args.seed, experts_on_host=True, with_norm=True,
                                 distinct_experts=args.distinct_experts) for l in range(n_layers)]
@@ -585,6 +589,7 @@ def run_streamed(args, cached: bool = False) -> dict:
                               f"and norms in HBM",
                    "hbm_expert_cache_gb": args.cache_gb if cached else None,
                    "copy_ahead_overlap_floor": args.overlap_floor,
+                   "extra_depth": args.extra_depth, "prob_resident": bool(args.prob_resident),
                    "tokens_input": (f"correlated: base + {args.token_noise} x N(0,1) per token" if cached
                                     else "independent N(0,1) tokens")},
         "roofline": {"bound": "pcie", "kernel": "hipMemcpyAsync host->device", "achieved": round(achieved, 1),
@@ -606,6 +611,73 @@ def run_streamed(args, cached: bool = False) -> dict:
     h.free()
     for L in layers:
         L.free()
+    return res
+
+
+def run_streamed_prefill(args) -> dict:
+    """One full-shape layer, a prefill chunk of --prefill-tokens tokens, routed
+    experts in pinned host RAM and the default slot pool (two layers' worth of
+    selections): the batch's distinct experts cross PCIe a wave at a time."""
+    shape = synth.LayerShape(**FULL)
+    T = args.prefill_tokens
+    capi.call("hfmoe_configure", shape.config(max_tokens=T))
+    layer = synth.DeviceLayer(shape, layer=0, seed=args.seed, experts_on_host=True,
+                              distinct_experts=args.distinct_experts)
+    x = synth.make_x_dev(T, shape.hidden, seed=args.seed)
+    out = capi.DeviceBuffer(T * shape.hidden * 4)
+    fwd = capi.load().hfmoe_moe_forward
+
+    def step():
+        rc = fwd(0, x.ptr, T, out.ptr, None)
+        if rc:
+            capi.check(rc)
+
+    for _ in range(args.warmup):
+        step()
+    capi.call("hfmoe_synchronize")
+    p0, a0 = C.c_uint64(), C.c_uint64()
+    capi.call("hfmoe_stats", C.byref(p0), C.byref(a0))
+    n0 = stream_counters()
+    sec = time_steps(step, args.steps, 0)
+    p1, a1 = C.c_uint64(), C.c_uint64()
+    capi.call("hfmoe_stats", C.byref(p1), C.byref(a1))
+    n1 = stream_counters()
+    cache = {c: (n1[c] - n0[c]) // args.steps for c in n1 if c != "slots"}
+    cache["slots"] = n1["slots"]
+    prof, sec_prof = profiled_pass(step, args.steps)
+    pcie = (p1.value - p0.value) / args.steps
+    nbytes = shape.top_k * shape.expert_bytes
+    src = capi.PinnedBuffer(nbytes)
+    dst = capi.DeviceBuffer(nbytes)
+    capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        capi.call("hfmoe_memcpy_h2d", dst.ptr, src.ptr, nbytes)
+    h2d_gbs = 5 * nbytes / (time.perf_counter() - t0) / 1e9
+    achieved = pcie / sec / 1e9
+    res = {
+        "value": T / sec,
+        "ms_per_step": sec * 1e3,
+        "config": {"workload": "moe_streamed_prefill", "tokens": T, "layers": 1, "hidden": shape.hidden,
+                   "moe_intermediate": shape.inter, "routed_experts": shape.n_experts,
+                   "shared_experts": shape.n_shared, "top_k": shape.top_k, "n_group": shape.n_group,
+                   "topk_group": shape.topk_group,
+                   "weights": f"routed experts in pinned host RAM ({args.distinct_experts} distinct weight sets, "
+                              f"every expert its own cache key); router and shared expert in HBM",
+                   "slot_pool": "default: 2 x top_k slots, waves of top_k experts"},
+        "roofline": {"bound": "pcie", "kernel": "hipMemcpyAsync host->device", "achieved": round(achieved, 1),
+                     "peak": round(h2d_gbs, 1), "unit": "GB/s", "frac": round(achieved / h2d_gbs, 4),
+                     "traffic": int(pcie), "peak_source": "measured pinned copy of 8 experts"},
+        "pcie_bytes_per_call": int(pcie),
+        "expert_cache_per_call": cache,
+        "ms_per_step_with_kernel_events": sec_prof * 1e3,
+        "kernels": kernel_table(prof, {}),
+    }
+    src.free()
+    dst.free()
+    x.free()
+    out.free()
+    layer.free()
     return res
 
 
@@ -767,6 +839,7 @@ METRICS = {
     "batched": "MoE-layer batched-decode tokens/s + HBM GB/s at d=6144, 256e top-8, T=64 Zipf(1.1)",
     "prefill": "MoE-layer prefill tokens/s + BF16 MFMA TFLOP/s at d=6144, 256e top-8, T=4096",
     "streamed": "8-layer streamed-expert decode tokens/s + PCIe GB/s at d=6144, 256e top-8",
+    "streamed_prefill": "streamed-expert prefill tokens/s + PCIe GB/s at d=6144, 256e top-8, T=4096",
     "dense": "dense-MLP layer tokens/s + HBM GB/s at d=6144, intermediate 12288",
     "lm_head": "LM head + greedy argmax tokens/s + HBM GB/s at d=6144, vocab 154880",
     "streamed_cached": "8-layer streamed-expert decode tokens/s with an HBM expert cache and next-layer "
@@ -780,8 +853,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "dense", "lm_head",
-                             "load", "plugin", "copy"])
+                    choices=["decode", "batched", "prefill", "streamed", "streamed_cached", "streamed_prefill",
+                             "dense", "lm_head", "load", "plugin", "copy"])
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--distinct-experts", type=int, default=32,
                     help="streamed: distinct expert weight sets per layer (bounds pinned host memory)")
@@ -791,7 +864,12 @@ def main() -> int:
                     help="streamed_cached: per-token deviation from the shared base input")
     ap.add_argument("--overlap-floor", type=float, default=0.5,
                     help="streamed: winner-overlap EMA below which next-layer copy-ahead is skipped")
+    ap.add_argument("--extra-depth", type=int, default=0,
+                    help="streamed: router-probability extra copy-ahead depth (setRouterPrefetch)")
+    ap.add_argument("--prob-resident", action="store_true",
+                    help="streamed: pin experts within 10%% of the layer's top routing weight (setRouterPrefetch)")
     ap.add_argument("--dense-tokens", type=int, default=1, help="dense: tokens per call")
+    ap.add_argument("--prefill-tokens", type=int, default=4096, help="streamed_prefill: tokens per call")
     ap.add_argument("--load-experts", type=int, default=64,
                     help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -805,7 +883,7 @@ def main() -> int:
               f"(the MoE block runs on a single MI355X; sharding is design-only)", file=sys.stderr)
         return 2
     defaults = {"decode": (200, 20), "batched": (100, 10), "prefill": (20, 3), "streamed": (20, 3),
-                "streamed_cached": (30, 10), "dense": (100, 10), "lm_head": (100, 10), "load": (1, 0),
+                "streamed_cached": (30, 10), "streamed_prefill": (3, 1), "dense": (100, 10), "lm_head": (100, 10), "load": (1, 0),
                 "plugin": (200, 20), "copy": (5, 0)}
     d_steps, d_warm = defaults[args.workload]
     args.steps = d_steps if args.steps is None else args.steps
@@ -823,6 +901,8 @@ def main() -> int:
         res = run_lm_head(args)
     elif args.workload in ("streamed", "streamed_cached"):
         res = run_streamed(args, cached=args.workload == "streamed_cached")
+    elif args.workload == "streamed_prefill":
+        res = run_streamed_prefill(args)
     else:
         res = run_grouped(args, args.workload)
     line = {"metric": METRICS[args.workload], "value": round(res.pop("value"), 2), "unit": "tokens/s",

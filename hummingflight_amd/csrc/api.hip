@@ -381,8 +381,21 @@ int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out
     LayerState& L = it->second;
     if (L.dense) return fail(HFMOE_ERR_INVALID_ARGUMENT, "layer %d is a dense MLP layer", layer);
     if (L.location == HFMOE_EXPERTS_HOST_PINNED) {
-        if (T != 1) return fail(HFMOE_ERR_UNSUPPORTED, "streamed experts support T=1 only");
-        return streamed_forward_t1(layer, L, x_dev, out_dev, s, dbg);
+        if (T == 1) return streamed_forward_t1(layer, L, x_dev, out_dev, s, dbg);
+        if (g.gws.xh) return streamed_forward_batch(layer, L, x_dev, T, out_dev, s, dbg);
+        // Shapes the grouped GEMM does not tile: token by token.
+        for (int t = 0; t < T; ++t) {
+            hfmoe_route_debug d1{};
+            if (dbg) {
+                d1.logits_dev = dbg->logits_dev ? dbg->logits_dev + (size_t)t * g.cfg.E : nullptr;
+                d1.idx_dev = dbg->idx_dev ? dbg->idx_dev + (size_t)t * g.cfg.k : nullptr;
+                d1.weight_dev = dbg->weight_dev ? dbg->weight_dev + (size_t)t * g.cfg.k : nullptr;
+            }
+            rc = streamed_forward_t1(layer, L, x_dev + (size_t)t * g.cfg.d, out_dev + (size_t)t * g.cfg.d, s,
+                                     dbg ? &d1 : nullptr);
+            if (rc) return rc;
+        }
+        return HFMOE_OK;
     }
     if (T == 1) return forward_t1(L, x_dev, out_dev, s, dbg);
     return forward_grouped(L, x_dev, T, out_dev, s, dbg);

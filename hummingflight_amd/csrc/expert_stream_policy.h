@@ -23,6 +23,20 @@
 //    hottest routed expert gets a one-sweep boost (:279-292).  The reference
 //    then fills the guess list with hot experts only up to the size of the
 //    list it already has, which adds none (:190-218); that is kept.
+//
+//  * the router-probability mode (Scheduler::setRouterPrefetch,
+//    scheduler.cpp:148-156, rules :320-352), given each winner's routing
+//    weight: extra_depth adds this token's winners not already guessed, by
+//    descending weight, as further layer L+1 copy-aheads (after the overlap
+//    gate, so also when it is closed); prob_resident keeps a running maximum
+//    of the layer's routing weights and pins a resident winner whose weight is
+//    at least 0.9 x that maximum once it has been looked up twice before (a
+//    pinned slot is never a victim while an unpinned one is available).
+//
+// Order of one call, the reference's (moeLayer calls onLayerRouterDone,
+// glm_forward.cpp:548, before the expert loop's getExpertPtr, :564, :623):
+// route_done (history, heat and boost, pins, guesses), then the demand
+// lookups in rank order, then the copy-aheads of the guesses.
 #pragma once
 
 #include <algorithm>
@@ -39,6 +53,8 @@ struct StreamPolicyOptions {
     float ema_alpha = 0.1f;        // heat blend, (0, 1]
     float overlap_floor = 0.5f;    // kSpecOverlapFloor (scheduler.cpp:51)
     float overlap_alpha = 0.5f;    // kSpecOverlapAlpha (scheduler.cpp:52)
+    int extra_depth = 0;           // prefetchExtraDepth (scheduler.cpp:148-156, 320-336)
+    bool prob_resident = false;    // probPriority: probability-weighted residency (:338-352)
 };
 
 struct StreamPolicyCounters {
@@ -50,6 +66,7 @@ struct StreamPolicyCounters {
     uint64_t pred_wasted = 0;    // staged entries evicted unused (prefetchWasted)
     uint64_t pred_resident = 0;  // predictions already resident: no copy
     uint64_t copies = 0;         // expert weight sets copied host -> HBM
+    uint64_t pinned = 0;         // resident experts pinned by the probability rule
 };
 
 inline uint64_t expert_key(int layer, int expert) {
@@ -67,6 +84,9 @@ public:
         protect_.assign(slots, 0);
         staged_.assign(slots, 0);
         used_.assign(slots, 0);
+        pinned_.assign(slots, 0);
+        access_.clear();
+        max_prob_.clear();
         where_.clear();
         head_ = tail_ = -1;
         last_topk_.clear();
@@ -86,6 +106,7 @@ public:
     int lookup(int layer, int expert, const int* claimed, int nclaimed, bool* copy) {
         const uint64_t k = expert_key(layer, expert);
         ++n.lookups;
+        ++access_[k];  // PlacementDirector::recordAccess in getExpertPtr (scheduler.cpp:652)
         int s = find(k);
         if (s >= 0) {
             ++n.hits;
@@ -103,10 +124,14 @@ public:
         return s;
     }
 
-    // Layer finished routing with selection topk[0..k).  Updates the routing
-    // history and returns the experts of layer + 1 to stage (empty when
-    // prefetch is off, next_streamed is false or the gate is closed).
-    std::vector<int> route_done(int layer, const int* topk, int k, bool next_streamed) {
+    // Layer finished routing with selection topk[0..k) and the winners'
+    // routing weights probs[0..k) (or null).  Updates the routing history,
+    // heat and pins, and returns the experts of layer + 1 to stage: empty when
+    // there is no next layer (has_next false: the reference stops there,
+    // scheduler.cpp:293-294), when prefetch is off or the next layer's experts
+    // are not streamed.
+    std::vector<int> route_done(int layer, const int* topk, const float* probs, int k, bool has_next,
+                                bool next_streamed) {
         std::vector<int> cur(topk, topk + k);
         std::vector<int>& last = last_topk_[layer];
         float& ema = overlap_[layer];
@@ -117,6 +142,10 @@ public:
             ema = opt.overlap_alpha * frac + (1.0f - opt.overlap_alpha) * ema;
         }
         last = cur;
+        if (opt.prob_resident && probs) {
+            float& mx = max_prob_[layer];
+            for (int r = 0; r < k; ++r) mx = std::max(mx, probs[r]);
+        }
         if (opt.ema_predictor) {
             const float a = opt.ema_alpha > 0.0f && opt.ema_alpha <= 1.0f ? opt.ema_alpha : 0.1f;
             int best = -1;
@@ -131,11 +160,30 @@ public:
             }
             if (best >= 0) boost(expert_key(layer, best), 1);
         }
-        if (!opt.prefetch || !next_streamed) return {};
+        if (!has_next) return {};
         auto it = last_topk_.find(layer + 1);
         std::vector<int> guess = (it != last_topk_.end() && !it->second.empty()) ? it->second : cur;
         auto ot = overlap_.find(layer + 1);
         if ((ot == overlap_.end() ? 0.0f : ot->second) < opt.overlap_floor) guess.clear();
+        if (opt.extra_depth > 0 && probs) {
+            // This token's winners by descending weight (ties in rank order),
+            // skipping those already guessed.
+            std::vector<int> order;
+            for (int r = 0; r < k; ++r)
+                if (probs[r] > 0.0f && std::find(guess.begin(), guess.end(), topk[r]) == guess.end())
+                    order.push_back(r);
+            std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return probs[a] > probs[b]; });
+            for (int i = 0; i < (int)order.size() && i < opt.extra_depth; ++i) guess.push_back(topk[order[i]]);
+        }
+        if (opt.prob_resident && probs) {
+            const float mx = max_prob_[layer];
+            for (int r = 0; mx > 0.0f && r < k; ++r) {
+                const uint64_t key = expert_key(layer, topk[r]);
+                auto ac = access_.find(key);
+                if (probs[r] >= 0.9f * mx && ac != access_.end() && ac->second >= 2) pin(key);
+            }
+        }
+        if (!opt.prefetch || !next_streamed) return {};
         return guess;
     }
 
@@ -164,13 +212,25 @@ public:
             unlink(s);
             key_[s] = kEmpty;
             protect_[s] = 0;
-            staged_[s] = used_[s] = 0;
+            staged_[s] = used_[s] = pinned_[s] = 0;
         }
         last_topk_.erase(layer);
         overlap_.erase(layer);
+        max_prob_.erase(layer);
+        for (auto it = access_.begin(); it != access_.end();)
+            it = (int)(uint32_t)(it->first >> 32) == layer ? access_.erase(it) : std::next(it);
         for (auto it = heat_.begin(); it != heat_.end();)
             it = (int)(uint32_t)(it->first >> 32) == layer ? heat_.erase(it) : std::next(it);
     }
+
+    // Pin a resident entry: no victim while an unpinned slot can be taken.
+    void pin(uint64_t key) {
+        const int s = find(key);
+        if (s < 0 || pinned_[s]) return;
+        pinned_[s] = 1;
+        ++n.pinned;
+    }
+    bool is_pinned(int slot) const { return pinned_[slot] != 0; }
 
     // Soft boost: most recent, and survives `cycles` eviction sweeps.
     void boost(uint64_t key, int cycles) {
@@ -207,15 +267,18 @@ private:
         return false;
     }
     // An empty slot (lowest index) first.  Else one sweep from the least
-    // recent end: claimed slots are skipped, a protected one spends one
-    // protection and survives, the first other one is the victim.  A demand
-    // lookup must get a slot, so when the sweep finds none it takes the least
-    // recent unclaimed slot regardless of protection; a copy-ahead gives up.
+    // recent end: claimed and pinned slots are skipped, a protected one spends
+    // one protection and survives, the first other one is the victim.  A
+    // demand lookup must get a slot, so when the sweep finds none it takes the
+    // least recent unclaimed unpinned slot regardless of protection, and when
+    // every unclaimed slot is pinned, the least recent of those (unpinning
+    // it: the reference's host cache would serve the expert uncached); a
+    // copy-ahead gives up.
     int victim(const int* claimed, int nclaimed, bool must) {
         for (int s = 0; s < slots(); ++s)
             if (key_[s] == kEmpty && !contains(claimed, nclaimed, s)) return s;
         for (int s = tail_; s >= 0; s = prev_[s]) {
-            if (contains(claimed, nclaimed, s)) continue;
+            if (contains(claimed, nclaimed, s) || pinned_[s]) continue;
             if (protect_[s] > 0) {
                 --protect_[s];
                 continue;
@@ -223,6 +286,8 @@ private:
             return s;
         }
         if (!must) return -1;
+        for (int s = tail_; s >= 0; s = prev_[s])
+            if (!contains(claimed, nclaimed, s) && !pinned_[s]) return s;
         for (int s = tail_; s >= 0; s = prev_[s])
             if (!contains(claimed, nclaimed, s)) return s;
         return -1;
@@ -236,6 +301,7 @@ private:
         key_[s] = k;
         where_[k] = s;
         protect_[s] = 0;
+        pinned_[s] = 0;
         staged_[s] = staged;
         used_[s] = !staged;
         push_front(s);
@@ -243,7 +309,9 @@ private:
 
     std::vector<uint64_t> key_;
     std::vector<int> prev_, next_, protect_;
-    std::vector<uint8_t> staged_, used_;
+    std::vector<uint8_t> staged_, used_, pinned_;
+    std::unordered_map<uint64_t, int> access_;  // demand lookups per (layer, expert)
+    std::map<int, float> max_prob_;             // running maximum routing weight per layer
     std::unordered_map<uint64_t, int> where_;
     int head_ = -1, tail_ = -1;
     std::map<int, std::vector<int>> last_topk_;

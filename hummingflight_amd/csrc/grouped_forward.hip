@@ -108,12 +108,11 @@ int grouped_workspace_alloc() {
         if (e_ != hipSuccess) return fail_hip(e_, what); \
     } while (0)
 
-int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
-                    const hfmoe_route_debug* dbg) {
-    if (!g.gws.xh) return forward_tokenwise(L, x, T, out, s, dbg);
+int grouped_tile_rows(int T) { return expert_tile_rows(T); }
+
+int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     const Cfg& c = g.cfg;
     GroupedWorkspace& w = g.gws;
-    const int P = T * c.k;
     const int shared_rows = c.n_shared > 0 ? T : 0;
     const int TR = expert_tile_rows(T);
     Pending p;
@@ -149,6 +148,16 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
                                     w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0,
                                     w.ntiles, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
                     "dispatch");
+    return HFMOE_OK;
+}
+
+int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
+    const Cfg& c = g.cfg;
+    GroupedWorkspace& w = g.gws;
+    const int P = T * c.k;
+    const int shared_rows = c.n_shared > 0 ? T : 0;
+    const int TR = expert_tile_rows(T);
+    Pending p;
 
     // Gate/up of every group: the routed experts' (token, rank) rows and the
     // shared expert's token rows (group E), one launch.
@@ -167,7 +176,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     gu.a_lo = w.xl;
     gu.a_lo_flag = w.lo_flag;
     gu.a_rowmap = w.row_token;
-    gu.b_tab = L.dev.etab;
+    gu.b_tab = etab;
     gu.b_which = 0;
     gu.b_ld = c.d;
     gu.h_hi = w.hh;
@@ -192,7 +201,7 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.rows_total = P + shared_rows;
     dn.a_hi = w.hh;
     dn.a_lo = w.hl;
-    dn.b_tab = L.dev.etab;
+    dn.b_tab = etab;
     dn.b_which = 2;
     dn.b_ld = c.I;
     dn.out_f32 = w.y;
@@ -201,10 +210,25 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
+    return HFMOE_OK;
+}
 
+int grouped_combine(int T, float* out, hipStream_t s) {
+    const Cfg& c = g.cfg;
+    const int P = T * c.k;
+    Pending p;
     prof_begin(p, "combine", s);
-    HF_CHECK_LAUNCH(launch_combine(g.ws.wts, w.y, T, c.k, c.d, shared_rows ? P : -1, out, s), "combine");
-    return copy_debug(dbg, T, s);
+    HF_CHECK_LAUNCH(launch_combine(g.ws.wts, g.gws.y, T, c.k, c.d, c.n_shared > 0 ? P : -1, out, s), "combine");
+    return HFMOE_OK;
+}
+
+int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                    const hfmoe_route_debug* dbg) {
+    if (!g.gws.xh) return forward_tokenwise(L, x, T, out, s, dbg);
+    int rc = grouped_route(L, x, T, s);
+    if (!rc) rc = grouped_experts(L.dev.etab, T, s);
+    if (!rc) rc = grouped_combine(T, out, s);
+    return rc ? rc : copy_debug(dbg, T, s);
 }
 
 }  // namespace hf

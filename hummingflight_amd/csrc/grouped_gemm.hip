@@ -384,6 +384,13 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
 // also leaves it more registers).
 enum { kLoNone = 0, kLoByFlag = 1, kLoAlways = 2 };
 
+// A group whose weight-table entry is null takes no part in this launch: its
+// tiles are skipped (streamed experts are multiplied a wave of groups at a
+// time, the other groups' entries left null).
+__device__ __forceinline__ bool group_absent(const GemmArgs& a, int g) {
+    return a.b_tab && a.b_tab[3 * g + a.b_which] == nullptr;
+}
+
 // WAVES = 4: 128-row tiles, two workgroups per CU.
 template <int EPI, int LOM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
@@ -400,6 +407,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
         // Row blocks of this wavefront in the item's tile (wave-uniform).
         const int mt = item / a.ksplit / a.n_tiles;
         const int g = a.tile_group ? a.tile_group[mt] : 0;
+        if (group_absent(a, g)) continue;  // workgroup-uniform: no barrier is skipped by some waves only
         const int row0 = a.tile_row0 ? a.tile_row0[mt] : mt * 32 * WAVES;
         const int row_end = a.group_end ? a.group_end[g] : a.rows_total;
         const int wrows = min(max(min(32 * WAVES, row_end - row0) - 32 * wave, 0), 32);
@@ -651,6 +659,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
     auto run = [&](int item) {
+        if (group_absent(a, a.tile_group ? a.tile_group[item / a.ksplit / a.n_tiles] : 0)) return;
         if (LOM != kLoNone && use_lo)
             gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
         else
@@ -738,6 +747,10 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
 __global__ void clear_u32_kernel(unsigned* p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0u;
+}
+
+hipError_t launch_clear_u32(unsigned* p, int n, hipStream_t s) {
+    return launch(clear_u32_kernel, dim3((n + 63) / 64), dim3(64), 0, s, p, n);
 }
 
 // Router logits from split-K partials (summed in split order) and score pairs.

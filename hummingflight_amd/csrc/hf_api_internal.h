@@ -99,13 +99,29 @@ struct StreamPool {
     std::vector<hipEvent_t> copied;   // per slot: H2D done (copy stream)
     std::vector<hipEvent_t> consumed; // per slot: last kernel reading it done
     ExpertStreamPolicy policy;
-    int* idx_host = nullptr;          // pinned [k] selected experts readback
-    float* w_host = nullptr;
-    const uint16_t** etab_host = nullptr;  // pinned [3*k] slot pointers for the table
+    // Small transfers between the compute stream and the host go through
+    // mapped pinned memory, read or written by a kernel on that stream: a DMA
+    // copy there could queue behind expert weight copies.
+    int* idx_host = nullptr;          // pinned, mapped [k] selected experts readback
+    float* w_host = nullptr;          // pinned, mapped [k] their routing weights
+    const uint16_t** etab_host = nullptr;  // pinned, mapped [3*k] slot pointers for the table
+    int* idx_host_dev = nullptr;      // device addresses of the three
+    float* w_host_dev = nullptr;
+    const uint16_t** etab_host_dev = nullptr;
     const uint16_t** etab_dev = nullptr;   // device [3*k] slot pointers of this call
     int* iota_dev = nullptr;               // device [k] = 0..k-1 (slot order)
     float* shared_out = nullptr;           // device [d] shared-expert output
     hipEvent_t routed = nullptr;
+    // Multi-token calls: the batch's selections read back, and one pinned
+    // staging table of 3 * (E + 1) slot pointers per wave of experts (a wave's
+    // table is copied to the layer's device table while the host fills the next).
+    int* idx_batch_host = nullptr;         // pinned, mapped [max_tokens * k]
+    float* w_batch_host = nullptr;         // pinned, mapped [max_tokens * k] routing weights
+    int* idx_batch_host_dev = nullptr;
+    float* w_batch_host_dev = nullptr;
+    const uint16_t** wave_tabs = nullptr;  // pinned, mapped [max_waves][3 * (E + 1)]
+    const uint16_t** wave_tabs_dev = nullptr;  // its device address (a kernel copies a table in)
+    int max_waves = 0;
 };
 
 struct State {
@@ -177,6 +193,14 @@ int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s);
 // grouped_forward.hip
 int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                     const hfmoe_route_debug* dbg);
+// The three phases of forward_grouped (multi-token path, grouped workspace
+// allocated): routing (x split, router, selection, dispatch), the expert
+// gate/up and down GEMMs of the groups whose etab entries are not null (3 per
+// group, E + 1 groups, the shared expert last), and the weighted combine.
+int grouped_route(LayerState& L, const float* x, int T, hipStream_t s);
+int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s);
+int grouped_combine(int T, float* out, hipStream_t s);
+int grouped_tile_rows(int T);
 int grouped_workspace_alloc();
 void grouped_workspace_free();
 int gemm_blocks(int tile_rows);
@@ -190,11 +214,18 @@ hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, int M, int K, f
 // streamed.hip
 int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hipStream_t s,
                         const hfmoe_route_debug* dbg);
+// T > 1 over the grouped GEMMs: the batch's distinct experts in waves that fit
+// the slot pool (grouped workspace required).
+int streamed_forward_batch(int layer, LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                           const hfmoe_route_debug* dbg);
 void stream_pool_release();
 // misc kernels
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s);
 hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s);
 hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s);
+// dst[0, n) = src[0, n) by a kernel (either may be mapped pinned host memory).
+hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, size_t n, hipStream_t s);
+hipError_t launch_copy_u64(const uint64_t* src, uint64_t* dst, size_t n, hipStream_t s);
 
 }  // namespace hf

@@ -69,6 +69,28 @@ hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s
     return launch(copy_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
 }
 
+__global__ void copy_u32_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, size_t n, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 64) blocks = 64;
+    return launch(copy_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+}
+
+__global__ void copy_u64_kernel(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+hipError_t launch_copy_u64(const uint64_t* src, uint64_t* dst, size_t n, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 64) blocks = 64;
+    return launch(copy_u64_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+}
+
 hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, int d, float eps,
                           hipStream_t s) {
     if (d > 8 * kNormThreads) return hipErrorInvalidValue;

@@ -20,6 +20,7 @@
 //         the routed gate/up and down GEMVs with out = routed sum + shared_out,
 //         record each slot's `consumed`.
 #include "hf_api_internal.h"
+#include "hf_grouped.h"
 
 #include <cstring>
 
@@ -39,7 +40,36 @@ void stream_pool_release() {
     if (P.etab_dev) hipFree(P.etab_dev);
     if (P.iota_dev) hipFree(P.iota_dev);
     if (P.shared_out) hipFree(P.shared_out);
+    if (P.idx_batch_host) hipHostFree(P.idx_batch_host);
+    if (P.w_batch_host) hipHostFree(P.w_batch_host);
+    if (P.wave_tabs) hipHostFree(P.wave_tabs);
     P = StreamPool{};
+}
+
+// Experts per wave of a multi-token call that needs `distinct` experts: all of
+// them when they fit the pool, else half the pool, so one wave's copies land
+// in the slots the wave before last released while the last wave computes.
+static int wave_size(int slots, int distinct) {
+    return distinct <= slots ? distinct : std::max(1, slots / 2);
+}
+
+// Coherent pinned host memory a kernel can read and write, and its device address.
+template <typename Ptr>
+static hipError_t mapped_alloc(Ptr* host, Ptr* dev, size_t bytes) {
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(host), bytes, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(dev), (void*)*host, 0);
+    return e;
+}
+
+// Routing of n pairs (ids, weights) from the workspace to mapped host memory,
+// by a kernel on s; then `routed` is recorded on s.
+static hipError_t routing_to_host(int* idx_dev_view, float* w_dev_view, size_t n, hipStream_t s) {
+    hipError_t e = launch_copy_u32(reinterpret_cast<const uint32_t*>(g.ws.idx),
+                                   reinterpret_cast<uint32_t*>(idx_dev_view), n, s);
+    if (e == hipSuccess)
+        e = launch_copy_u32(reinterpret_cast<const uint32_t*>(g.ws.wts), reinterpret_cast<uint32_t*>(w_dev_view), n, s);
+    if (e == hipSuccess) e = hipEventRecord(g.pool.routed, s);
+    return e;
 }
 
 static int pool_init() {
@@ -67,12 +97,20 @@ static int pool_init() {
         if (e == hipSuccess) e = hipEventCreateWithFlags(&P.consumed[i], hipEventDisableTiming);
     }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&P.routed, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&P.idx_host), sizeof(int) * kMaxTopK, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&P.w_host), sizeof(float) * kMaxTopK, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&P.etab_host), sizeof(void*) * 3 * kMaxTopK, hipHostMallocDefault);
+    if (e == hipSuccess) e = mapped_alloc(&P.idx_host, &P.idx_host_dev, sizeof(int) * kMaxTopK);
+    if (e == hipSuccess) e = mapped_alloc(&P.w_host, &P.w_host_dev, sizeof(float) * kMaxTopK);
+    if (e == hipSuccess) e = mapped_alloc(&P.etab_host, &P.etab_host_dev, sizeof(void*) * 3 * kMaxTopK);
     if (e == hipSuccess) e = hipMalloc(&P.etab_dev, sizeof(void*) * 3 * kMaxTopK);
     if (e == hipSuccess) e = hipMalloc(&P.iota_dev, sizeof(int) * kMaxTopK);
     if (e == hipSuccess) e = hipMalloc(&P.shared_out, sizeof(float) * c.d);
+    if (e == hipSuccess && g.max_tokens > 1) {
+        P.max_waves = (c.E + wave_size(slots, c.E + 1) - 1) / wave_size(slots, c.E + 1) + 1;
+        e = mapped_alloc(&P.idx_batch_host, &P.idx_batch_host_dev, sizeof(int) * (size_t)g.max_tokens * c.k);
+        if (e == hipSuccess)
+            e = mapped_alloc(&P.w_batch_host, &P.w_batch_host_dev, sizeof(float) * (size_t)g.max_tokens * c.k);
+        if (e == hipSuccess)
+            e = mapped_alloc(&P.wave_tabs, &P.wave_tabs_dev, sizeof(void*) * 3 * (size_t)(c.E + 1) * P.max_waves);
+    }
     if (e == hipSuccess) {
         int iota[kMaxTopK];
         for (int i = 0; i < kMaxTopK; ++i) iota[i] = i;
@@ -117,8 +155,7 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
     e = launch_select(g.ws.scores, 1, c, g.ws.idx, g.ws.wts, s);
     prof_end(p, s);
     if (e != hipSuccess) return fail_hip(e, "select launch");
-    e = hipMemcpyAsync(P.idx_host, g.ws.idx, sizeof(int) * c.k, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipEventRecord(P.routed, s);
+    e = routing_to_host(P.idx_host_dev, P.w_host_dev, c.k, s);
     if (e != hipSuccess) return fail_hip(e, "routing readback");
 
     // Shared expert while the selected experts cross PCIe.
@@ -141,12 +178,21 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
 
     e = hipEventSynchronize(P.routed);
     if (e != hipSuccess) return fail_hip(e, "wait for routing");
+    for (int r = 0; r < c.k; ++r)
+        if (P.idx_host[r] < 0 || P.idx_host[r] >= c.E)
+            return fail(HFMOE_ERR_HIP, "router produced expert id %d", P.idx_host[r]);
 
-    int used[2 * kMaxTopK];
+    // The scheduler hears the routing first (history, heat, pins, guesses for
+    // the next layer), then the layer looks its experts up.
+    auto nx = g.layers.find(layer + 1);
+    const bool has_next = nx != g.layers.end();
+    const bool next_streamed = has_next && nx->second.location == HFMOE_EXPERTS_HOST_PINNED;
+    const std::vector<int> guess = P.policy.route_done(layer, P.idx_host, P.w_host, c.k, has_next, next_streamed);
+
+    int used[2 * kMaxTopK + kMaxTopK];
     const size_t proj = (size_t)c.I * c.d;
     for (int r = 0; r < c.k; ++r) {
         const int eid = P.idx_host[r];
-        if (eid < 0 || eid >= c.E) return fail(HFMOE_ERR_HIP, "router produced expert id %d", eid);
         bool copy = false;
         const int slot = P.policy.lookup(layer, eid, used, r, &copy);
         if (slot < 0) return fail(HFMOE_ERR_HIP, "expert slot pool exhausted");
@@ -164,20 +210,18 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
     }
     // Copy-ahead of the next layer's predicted experts, queued behind this
     // layer's copies; slots this call uses (and earlier copy-aheads of the
-    // batch) are not victims.
-    auto nx = g.layers.find(layer + 1);
-    const bool next_streamed = nx != g.layers.end() && nx->second.location == HFMOE_EXPERTS_HOST_PINNED;
-    const std::vector<int> guess = P.policy.route_done(layer, P.idx_host, c.k, next_streamed);
+    // call) are not victims.
     int nclaimed = c.k;
     for (int eid : guess) {
-        if (eid < 0 || eid >= c.E || nclaimed >= 2 * kMaxTopK) continue;
+        if (eid < 0 || eid >= c.E || nclaimed >= (int)(sizeof used / sizeof used[0])) continue;
         const int slot = P.policy.stage(layer + 1, eid, used, nclaimed);
         if (slot < 0) continue;
         int rc2 = copy_expert(nx->second, eid, slot);
         if (rc2) return rc2;
         used[nclaimed++] = slot;
     }
-    e = hipMemcpyAsync(P.etab_dev, P.etab_host, sizeof(void*) * 3 * c.k, hipMemcpyHostToDevice, s);
+    e = launch_copy_u64(reinterpret_cast<const uint64_t*>(P.etab_host_dev), reinterpret_cast<uint64_t*>(P.etab_dev),
+                        3 * (size_t)c.k, s);
     if (e != hipSuccess) return fail_hip(e, "slot table upload");
 
     Cfg cr = c;
@@ -207,6 +251,115 @@ int streamed_forward_t1(int layer, LayerState& L, const float* x, float* out, hi
     return HFMOE_OK;
 }
 
+int streamed_forward_batch(int layer, LayerState& L, const float* x, int T, float* out, hipStream_t s,
+                           const hfmoe_route_debug* dbg) {
+    int rc = pool_init();
+    if (rc) return rc;
+    StreamPool& P = g.pool;
+    const Cfg& c = g.cfg;
+    if (!P.idx_batch_host || !P.w_batch_host || !P.wave_tabs)
+        return fail(HFMOE_ERR_NOT_INITIALIZED, "multi-token staging buffers are not allocated");
+    rc = grouped_route(L, x, T, s);
+    if (rc) return rc;
+    const int npairs = T * c.k;
+    hipError_t e = routing_to_host(P.idx_batch_host_dev, P.w_batch_host_dev, (size_t)npairs, s);
+    if (e == hipSuccess) e = hipEventSynchronize(P.routed);
+    if (e != hipSuccess) return fail_hip(e, "routing readback");
+
+    // The batch's distinct experts, resident ones first (their waves compute
+    // while the others cross PCIe), then in order of first use.
+    std::vector<char> seen(c.E, 0);
+    std::vector<int> order, missing;
+    for (int i = 0; i < npairs; ++i) {
+        const int eid = P.idx_batch_host[i];
+        if (eid < 0 || eid >= c.E) return fail(HFMOE_ERR_HIP, "router produced expert id %d", eid);
+        if (seen[eid]) continue;
+        seen[eid] = 1;
+        (P.policy.find(expert_key(layer, eid)) >= 0 ? order : missing).push_back(eid);
+    }
+    order.insert(order.end(), missing.begin(), missing.end());
+    const int U = (int)order.size();
+    // The scheduler hears each token's routing in order, as the reference's
+    // token loop reports it (onLayerRouterDone per token); the copy-ahead
+    // follows the last token's guesses, queued after the batch's own copies.
+    auto nx = g.layers.find(layer + 1);
+    const bool has_next = nx != g.layers.end();
+    const bool next_streamed = has_next && nx->second.location == HFMOE_EXPERTS_HOST_PINNED;
+    std::vector<int> guess;
+    for (int t = 0; t < T; ++t)
+        guess = P.policy.route_done(layer, P.idx_batch_host + (size_t)t * c.k, P.w_batch_host + (size_t)t * c.k, c.k,
+                                    has_next, next_streamed && t == T - 1);
+    const int ws = wave_size(P.slots, U);
+    const int nwaves = (U + ws - 1) / ws;
+    if (nwaves > P.max_waves) return fail(HFMOE_ERR_HIP, "%d waves exceed the %d staged tables", nwaves, P.max_waves);
+    const size_t ntab = 3 * (size_t)(c.E + 1);
+    const size_t proj = (size_t)c.I * c.d;
+    const bool dynamic_items = grouped_tile_rows(T) == kPrefillTileRows;
+    std::vector<int> claimed;
+    // At most kWavesAhead waves of copies queued: before a wave's copies go in,
+    // the host waits for the copies of the wave that many places back.  With a
+    // prefill's whole ~700 copies queued at once they ran progressively slower
+    // (25 MB from 448 to ~630 us each) with gaps between them; two waves ahead
+    // keep the copy engine fed at the pinned copy rate.
+    constexpr int kWavesAhead = 2;
+    std::vector<int> wave_last_slot(nwaves, -1);
+    for (int wv = 0; wv < nwaves; ++wv) {
+        if (wv >= kWavesAhead && wave_last_slot[wv - kWavesAhead] >= 0) {
+            e = hipEventSynchronize(P.copied[wave_last_slot[wv - kWavesAhead]]);
+            if (e != hipSuccess) return fail_hip(e, "wait for an earlier wave's copies");
+        }
+        const uint16_t** tab = P.wave_tabs + (size_t)wv * ntab;
+        std::fill(tab, tab + ntab, nullptr);
+        claimed.clear();
+        for (int i = wv * ws; i < std::min(U, (wv + 1) * ws); ++i) {
+            const int eid = order[i];
+            bool copy = false;
+            const int slot = P.policy.lookup(layer, eid, claimed.data(), (int)claimed.size(), &copy);
+            if (slot < 0) return fail(HFMOE_ERR_HIP, "expert slot pool exhausted");
+            if (copy) {
+                rc = copy_expert(L, eid, slot);
+                if (rc) return rc;
+                wave_last_slot[wv] = slot;
+            }
+            claimed.push_back(slot);
+            const uint16_t* base = P.base + (size_t)slot * (P.slot_bytes / 2);
+            tab[3 * eid] = base;
+            tab[3 * eid + 1] = base + proj;
+            tab[3 * eid + 2] = base + 2 * proj;
+            e = hipStreamWaitEvent(s, P.copied[slot], 0);
+            if (e != hipSuccess) return fail_hip(e, "wait for expert H2D");
+        }
+        if (wv == 0 && c.n_shared > 0) {  // the shared expert (group E) is HBM-resident: first wave only
+            tab[3 * c.E] = L.dev.sg;
+            tab[3 * c.E + 1] = L.dev.su;
+            tab[3 * c.E + 2] = L.dev.sd;
+        }
+        // The table goes up by a small kernel reading the mapped pinned copy: a
+        // DMA copy here would queue behind the next wave's weight copies.
+        e = launch_copy_u64(reinterpret_cast<const uint64_t*>(P.wave_tabs_dev + (size_t)wv * ntab),
+                            reinterpret_cast<uint64_t*>(L.etab_dev), ntab, s);
+        if (e == hipSuccess && wv > 0 && dynamic_items)  // the dispatch zeroed them for the first wave
+            e = launch_clear_u32(g.gws.item_ctr, kItemCounters, s);
+        if (e != hipSuccess) return fail_hip(e, "wave table upload");
+        rc = grouped_experts(L.etab_dev, T, s);
+        if (rc) return rc;
+        for (int slot : claimed) {
+            e = hipEventRecord(P.consumed[slot], s);
+            if (e != hipSuccess) return fail_hip(e, "slot release");
+        }
+    }
+    for (int eid : guess) {
+        if (eid < 0 || eid >= c.E) continue;
+        const int slot = P.policy.stage(layer + 1, eid, claimed.data(), (int)claimed.size());
+        if (slot < 0) continue;
+        rc = copy_expert(nx->second, eid, slot);
+        if (rc) return rc;
+        claimed.push_back(slot);
+    }
+    rc = grouped_combine(T, out, s);
+    return rc ? rc : copy_debug(dbg, T, s);
+}
+
 }  // namespace hf
 
 using namespace hf;
@@ -219,12 +372,16 @@ int hfmoe_stream_set_options(const hfmoe_stream_options* o) {
     if (!o) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null options");
     if (!(o->ema_alpha > 0.0f && o->ema_alpha <= 1.0f) || !(o->overlap_alpha >= 0.0f && o->overlap_alpha <= 1.0f))
         return fail(HFMOE_ERR_INVALID_ARGUMENT, "ema_alpha must be in (0, 1] and overlap_alpha in [0, 1]");
+    if (o->extra_depth < 0 || o->extra_depth > kMaxTopK)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "extra_depth=%d must be in 0..%d", o->extra_depth, kMaxTopK);
     StreamPolicyOptions& so = g.stream_opt;
     so.prefetch = o->prefetch_next_layer != 0;
     so.ema_predictor = o->ema_predictor != 0;
     so.ema_alpha = o->ema_alpha;
     so.overlap_floor = o->overlap_floor;
     so.overlap_alpha = o->overlap_alpha;
+    so.extra_depth = o->extra_depth;
+    so.prob_resident = o->prob_resident != 0;
     g.pool.policy.opt = so;
     return HFMOE_OK;
 }
@@ -240,6 +397,8 @@ int hfmoe_stream_get_options(hfmoe_stream_options* o) {
     o->ema_alpha = so.ema_alpha;
     o->overlap_floor = so.overlap_floor;
     o->overlap_alpha = so.overlap_alpha;
+    o->extra_depth = so.extra_depth;
+    o->prob_resident = so.prob_resident;
     return HFMOE_OK;
 }
 
@@ -257,6 +416,7 @@ int hfmoe_stream_read_counters(hfmoe_stream_counters* out) {
     out->pred_wasted = n.pred_wasted;
     out->pred_resident = n.pred_resident;
     out->copies = n.copies;
+    out->pinned = n.pinned;
     out->slots = g.pool.slots;
     return HFMOE_OK;
 }

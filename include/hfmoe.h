@@ -216,7 +216,13 @@ typedef struct hfmoe_stream_options {
     float ema_alpha;              /* heat blend, (0, 1]; default 0.1 */
     float overlap_floor;          /* kSpecOverlapFloor (scheduler.cpp:51), default 0.5 */
     float overlap_alpha;          /* kSpecOverlapAlpha (scheduler.cpp:52), default 0.5 */
-    int32_t reserved[3];
+    /* Router-probability mode, Scheduler::setRouterPrefetch(prefetchExtraDepth,
+     * probPriority) (scheduler.cpp:148-156, rules :320-352); both off by default. */
+    int32_t extra_depth;          /* copy ahead this many more of the token's winners, by
+                                     descending routing weight, as next-layer guesses */
+    int32_t prob_resident;        /* 1: pin a resident winner whose routing weight is >= 0.9 x
+                                     the layer's running maximum once looked up twice before */
+    int32_t reserved;
 } hfmoe_stream_options;
 
 /* InferenceStats routedPredStaged / routedPredConsumed / prefetchWasted
@@ -230,6 +236,7 @@ typedef struct hfmoe_stream_counters {
     uint64_t pred_wasted;    /* copied-ahead experts evicted unused */
     uint64_t pred_resident;  /* predictions already resident (no copy) */
     uint64_t copies;         /* expert weight sets copied host -> HBM */
+    uint64_t pinned;         /* resident experts pinned by prob_resident */
     int32_t slots;           /* HBM slots in the pool (0 before the first streamed call) */
     int32_t reserved;
 } hfmoe_stream_counters;

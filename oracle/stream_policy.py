@@ -22,10 +22,19 @@ imports it).  It restates, per routing event of a streamed layer:
 * the guesses for layer+1 (predictNextLayerExperts, :180-219): the previous
   token's selection at layer+1, else this layer's selection; the popularity
   fill adds nothing because it stops at the size of that list (:195,207);
-  dropped when layer+1's overlap EMA is below the floor (:303-306).
+  dropped when layer+1's overlap EMA is below the floor (:303-306); none at
+  all past the last layer (:293-294).
+* the router-probability mode (setRouterPrefetch, :148-156; :320-352), from
+  the winners' routing weights: extra_depth more guesses from this token's
+  winners not yet guessed, by descending weight (after the gate); with
+  prob_resident a running per-layer maximum weight, and a resident winner with
+  weight >= 0.9 x that maximum and two earlier lookups is pinned (lru_.pin:
+  never evicted; here a demand lookup with only pinned candidates left takes
+  the least recent of them).
 
-The order of one call is the device path's: demand lookups in rank order,
-then the routing-history update, then copy-aheads of the guesses.
+The order of one call is the reference's (moeLayer reports the routing before
+its expert loop, glm_forward.cpp:548 before :564/:623): the routing-history
+update, then the demand lookups in rank order, then copy-aheads of the guesses.
 """
 from __future__ import annotations
 
@@ -40,10 +49,15 @@ class Options:
     ema_alpha: float = 0.1
     overlap_floor: float = 0.5
     overlap_alpha: float = 0.5
+    extra_depth: int = 0
+    prob_resident: bool = False
 
 
 COUNTERS = ("lookups", "hits", "misses", "pred_staged", "pred_consumed", "pred_wasted",
-            "pred_resident", "copies")
+            "pred_resident", "copies", "pinned")
+
+# Slots one call may hold: its k winners plus up to 2k copy-aheads.
+MAX_HELD = 24
 
 
 def _f32(v: float) -> float:
@@ -63,6 +77,9 @@ class StreamPolicy:
         self.protect = [0] * self.slots
         self.staged = [False] * self.slots
         self.used = [False] * self.slots
+        self.pinned = [False] * self.slots
+        self.access: dict[tuple[int, int], int] = {}
+        self.max_prob: dict[int, float] = {}
         self.last_topk: dict[int, list[int]] = {}
         self.overlap: dict[int, float] = {}
         self.heat: dict[tuple[int, int], float] = {}
@@ -83,13 +100,16 @@ class StreamPolicy:
             if self.key[s] is None and s not in held:
                 return s
         for s in list(self.recency):          # least recent first
-            if s in held:
+            if s in held or self.pinned[s]:
                 continue
             if self.protect[s] > 0:
                 self.protect[s] -= 1
                 continue
             return s
         if must:
+            for s in self.recency:
+                if s not in held and not self.pinned[s]:
+                    return s
             for s in self.recency:
                 if s not in held:
                     return s
@@ -100,6 +120,7 @@ class StreamPolicy:
             self.n["pred_wasted"] += 1
         self.key[s] = key
         self.protect[s] = 0
+        self.pinned[s] = False
         self.staged[s] = staged
         self.used[s] = not staged
         self._touch(s)
@@ -107,6 +128,7 @@ class StreamPolicy:
     def lookup(self, layer, expert, held):
         """Demand lookup: (slot, needs_copy)."""
         self.n["lookups"] += 1
+        self.access[(layer, expert)] = self.access.get((layer, expert), 0) + 1
         s = self.find((layer, expert))
         if s >= 0:
             self.n["hits"] += 1
@@ -127,7 +149,13 @@ class StreamPolicy:
             self.protect[s] = max(self.protect[s], cycles)
             self._touch(s)
 
-    def route_done(self, layer, topk, next_streamed):
+    def pin(self, key):
+        s = self.find(key)
+        if s >= 0 and not self.pinned[s]:
+            self.pinned[s] = True
+            self.n["pinned"] += 1
+
+    def route_done(self, layer, topk, probs=None, has_next=True, next_streamed=True):
         o = self.opt
         cur = list(topk)
         last = self.last_topk.get(layer, [])
@@ -139,6 +167,8 @@ class StreamPolicy:
             ema = _f32(_f32(oa * frac) + _f32(_f32(1.0 - oa) * ema))
         self.overlap[layer] = ema
         self.last_topk[layer] = cur
+        if o.prob_resident and probs is not None:
+            self.max_prob[layer] = max([self.max_prob.get(layer, 0.0)] + [_f32(p) for p in probs])
         if o.ema_predictor:
             a = _f32(o.ema_alpha if 0.0 < o.ema_alpha <= 1.0 else 0.1)
             best, best_heat = None, -1.0
@@ -150,11 +180,24 @@ class StreamPolicy:
                     best, best_heat = e, h
             if best is not None:
                 self.boost((layer, best), 1)
-        if not o.prefetch or not next_streamed:
+        if not has_next:
             return []
         guess = list(self.last_topk.get(layer + 1) or cur)
         if self.overlap.get(layer + 1, 0.0) < _f32(o.overlap_floor):
             guess = []
+        if o.extra_depth > 0 and probs is not None:
+            cand = [r for r in range(len(cur)) if _f32(probs[r]) > 0.0 and cur[r] not in guess]
+            cand.sort(key=lambda r: -_f32(probs[r]))  # stable: ties in rank order
+            guess += [cur[r] for r in cand[:o.extra_depth]]
+        if o.prob_resident and probs is not None:
+            mx = self.max_prob.get(layer, 0.0)
+            if mx > 0.0:
+                bar = _f32(_f32(0.9) * mx)
+                for e, p in zip(cur, probs):
+                    if _f32(p) >= bar and self.access.get((layer, e), 0) >= 2:
+                        self.pin((layer, e))
+        if not o.prefetch or not next_streamed:
+            return []
         return guess
 
     def stage(self, layer, expert, held):
@@ -170,16 +213,19 @@ class StreamPolicy:
         self.n["copies"] += 1
         return s
 
-    def call(self, layer, topk, next_streamed, n_experts=1 << 30):
-        """One streamed layer call: returns ([(slot, copy)], [(expert, slot)])."""
+    def call(self, layer, topk, next_layer, probs=None, n_experts=1 << 30):
+        """One streamed layer call; next_layer: 0 none, 1 streamed, 2 HBM-resident
+        (True / False read as 1 / 0).  Returns ([(slot, copy)], [(expert, slot)])."""
+        nl = int(next_layer)
+        guess = self.route_done(layer, topk, probs, nl != 0, nl == 1)
         held, looked = [], []
         for e in topk:
             s, c = self.lookup(layer, e, held)
             held.append(s)
             looked.append((s, c))
         staged = []
-        for e in self.route_done(layer, topk, next_streamed):
-            if e < 0 or e >= n_experts or len(held) >= 16:
+        for e in guess:
+            if e < 0 or e >= n_experts or len(held) >= MAX_HELD:
                 continue
             s = self.stage(layer + 1, e, held)
             if s < 0:

@@ -61,8 +61,9 @@ def run_chain(xs, d, k, E):
     return res
 
 
-@pytest.mark.parametrize("opts", [dict(), dict(overlap_floor=0.0, ema_predictor=1)],
-                         ids=["reference_defaults", "always_copy_ahead_with_popularity"])
+@pytest.mark.parametrize("opts", [dict(), dict(overlap_floor=0.0, ema_predictor=1),
+                                  dict(extra_depth=2, prob_resident=1)],
+                         ids=["reference_defaults", "always_copy_ahead_with_popularity", "router_probability_mode"])
 def test_streamed_cache_and_copy_ahead(hf, opts):
     d, k, E = DIMS["hidden"], DIMS["top_k"], DIMS["n_experts"]
     shape = synth.LayerShape(n_group=4, topk_group=2, **DIMS)
@@ -74,7 +75,8 @@ def test_streamed_cache_and_copy_ahead(hf, opts):
             for l in range(LAYERS)]
     xs = tokens(8, d, np.random.default_rng(SEED))
 
-    full = dict(prefetch_next_layer=1, ema_predictor=0, ema_alpha=0.1, overlap_floor=0.5, overlap_alpha=0.5)
+    full = dict(prefetch_next_layer=1, ema_predictor=0, ema_alpha=0.1, overlap_floor=0.5, overlap_alpha=0.5,
+                extra_depth=0, prob_resident=0)
     full.update(opts)
     set_options(**full)
     capi.call("hfmoe_stream_reset")
@@ -85,12 +87,13 @@ def test_streamed_cache_and_copy_ahead(hf, opts):
     # The oracle policy fed the same selections makes the same decisions.
     pol = StreamPolicy(SLOTS, Options(prefetch=True, ema_predictor=bool(full["ema_predictor"]),
                                       ema_alpha=full["ema_alpha"], overlap_floor=full["overlap_floor"],
-                                      overlap_alpha=full["overlap_alpha"]))
-    for r in got:
-        pol.call(r["layer"], r["idx"], r["layer"] + 1 < LAYERS)
+                                      overlap_alpha=full["overlap_alpha"], extra_depth=full["extra_depth"],
+                                      prob_resident=bool(full["prob_resident"])))
+    for r in got:  # the last layer has no next layer registered
+        pol.call(r["layer"], r["idx"], 1 if r["layer"] + 1 < LAYERS else 0, probs=r["w"].tolist())
     assert {c: n[c] for c in COUNTERS} == pol.n
     assert n["misses"] > 0 and n["hits"] > 0
-    if full["overlap_floor"] == 0.0:
+    if full["overlap_floor"] == 0.0 or full["extra_depth"]:
         assert n["pred_staged"] > 0 and n["pred_consumed"] > 0
 
     # Outputs: oracle per token (selection given the GPU's logits).
@@ -111,7 +114,8 @@ def test_streamed_cache_and_copy_ahead(hf, opts):
     assert read_counters()["pred_staged"] == 0
     for a, b in zip(got, again):
         assert np.array_equal(a["out"].view(np.uint32), b["out"].view(np.uint32))
-    set_options(prefetch_next_layer=1, ema_predictor=0, ema_alpha=0.1, overlap_floor=0.5, overlap_alpha=0.5)
+    set_options(prefetch_next_layer=1, ema_predictor=0, ema_alpha=0.1, overlap_floor=0.5, overlap_alpha=0.5,
+                extra_depth=0, prob_resident=0)
     for L in layers:
         L.free()
 

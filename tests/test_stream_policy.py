@@ -14,6 +14,7 @@ import random
 import shutil
 import subprocess
 
+import numpy as np
 import pytest
 
 from oracle.stream_policy import COUNTERS, Options, StreamPolicy
@@ -101,16 +102,68 @@ def test_oracle_carry_over_consumed_and_wasted():
 
 
 def test_oracle_popularity_boost_changes_victims():
-    calls = [(0, [0, 1]), (0, [2, 3]), (0, [4, 5])]
-    plain = StreamPolicy(4, Options(prefetch=False))
-    boosted = StreamPolicy(4, Options(prefetch=False, ema_predictor=True))
+    # Three slots.  Expert 0, routed at the first two calls, is the layer's
+    # hottest at the second and resident by then (the routing is reported
+    # before the lookups): its one-sweep protection makes the third call evict
+    # experts 1 and 2 instead of 1 and 0.
+    calls = [(0, [0, 1]), (0, [0, 2]), (0, [3, 4])]
+    plain = StreamPolicy(3, Options(prefetch=False))
+    boosted = StreamPolicy(3, Options(prefetch=False, ema_predictor=True))
     for layer, topk in calls:
         a = plain.call(layer, topk, False)[0]
         b = boosted.call(layer, topk, False)[0]
-    # Plain LRU evicts experts 0 and 1.  Boosted: 0 (first routed, hottest on a
-    # tie) and 2 are protected for one sweep, so 1 and 3 go instead.
-    assert a == [(0, True), (1, True)]
-    assert b == [(1, True), (3, True)]
+    assert a == [(1, True), (0, True)]
+    assert b == [(1, True), (2, True)]
+    assert boosted.find((0, 0)) == 0 and plain.find((0, 0)) == -1
+
+
+def test_oracle_extra_depth_copies_the_most_probable_winners():
+    # setRouterPrefetch(extra, ...): after the overlap gate (closed on the first
+    # token), this token's winners by descending routing weight become layer
+    # 1's guesses, up to extra_depth of them; ties keep rank order.
+    p = StreamPolicy(16, Options(extra_depth=2))
+    looked, staged = p.call(0, [3, 4, 5], 1, probs=[0.2, 0.5, 0.3])
+    assert [s for s, _ in looked] == [0, 1, 2] and staged == [(4, 3), (5, 4)]
+    assert p.n["pred_staged"] == 2
+    p = StreamPolicy(16, Options(extra_depth=3))
+    assert p.call(0, [3, 4, 5], 1, probs=[0.4, 0.4, 0.4])[1] == [(3, 3), (4, 4), (5, 5)]
+    # No next layer: nothing (the reference stops before its guesses).
+    p = StreamPolicy(16, Options(extra_depth=2))
+    assert p.call(0, [3, 4, 5], 0, probs=[0.2, 0.5, 0.3])[1] == []
+    # An open gate's guesses come first and are not repeated.
+    p = StreamPolicy(16, Options(extra_depth=1, overlap_floor=0.0))
+    assert p.call(0, [3, 4], 1, probs=[0.3, 0.6])[1] == [(3, 2), (4, 3)]
+
+
+def test_oracle_probability_pins_survive_eviction():
+    # probPriority: expert 0 (weight 0.95 >= 0.9 x the layer's running maximum
+    # 1.0, looked up twice before) is pinned at its third call, so three later
+    # cold experts evict experts 1 and 2 around it; without the rule, or with
+    # no next layer (the reference returns before its pin rule), expert 0 goes.
+    def run(opt, next_layer):
+        p = StreamPolicy(3, opt)
+        for e, w in [(0, 1.0), (0, 1.0), (0, 0.95), (1, 0.5), (2, 0.5)]:
+            p.call(0, [e], next_layer, probs=[w])
+        return p, p.call(0, [3], next_layer, probs=[0.5])[0]
+    p, looked = run(Options(prefetch=False, prob_resident=True), 2)
+    assert looked == [(1, True)] and p.n["pinned"] == 1 and p.find((0, 0)) == 0
+    for opt, nl in [(Options(prefetch=False), 2), (Options(prefetch=False, prob_resident=True), 0)]:
+        p, looked = run(opt, nl)
+        assert looked == [(0, True)] and p.n["pinned"] == 0
+    # Weight 0.85 < 0.9: no pin.
+    p = StreamPolicy(3, Options(prefetch=False, prob_resident=True))
+    for e, w in [(0, 1.0), (0, 1.0), (0, 0.85)]:
+        p.call(0, [e], 2, probs=[w])
+    assert p.n["pinned"] == 0
+
+
+def test_oracle_demand_lookup_takes_a_pinned_slot_when_nothing_else_is_left():
+    p = StreamPolicy(2, Options(prefetch=False, prob_resident=True))
+    for _ in range(3):
+        p.call(0, [0, 1], 2, probs=[1.0, 1.0])
+    assert p.n["pinned"] == 2
+    looked, _ = p.call(0, [5], 2, probs=[1.0])
+    assert looked == [(0, True)] and p.find((0, 0)) == -1  # least recent of the pinned
 
 
 def correlated_history(rng, layers, tokens, k, n_experts, p_change):
@@ -145,17 +198,23 @@ def test_library_policy_matches_oracle(driver):
         slots = rng.choice([2 * k, 3 * k, layers * k, 2 * layers * k + 1])
         opt = Options(prefetch=rng.random() < 0.8, ema_predictor=rng.random() < 0.5,
                       ema_alpha=rng.choice([0.1, 0.5, 1.0]), overlap_floor=rng.choice([0.0, 0.3, 0.5, 0.8]),
-                      overlap_alpha=rng.choice([0.5, 0.3, 1.0]))
+                      overlap_alpha=rng.choice([0.5, 0.3, 1.0]), extra_depth=rng.choice([0, 0, 1, 3, 8]),
+                      prob_resident=rng.random() < 0.5)
         hist = correlated_history(rng, layers, 12, k, 24, rng.choice([0.0, 0.2, 0.5, 1.0]))
         lines = [f"opt {int(opt.prefetch)} {int(opt.ema_predictor)} {opt.ema_alpha} {opt.overlap_floor} "
-                 f"{opt.overlap_alpha}", f"reset {slots}"]
+                 f"{opt.overlap_alpha} {opt.extra_depth} {int(opt.prob_resident)}", f"reset {slots}"]
         p = StreamPolicy(slots, opt)
         want = []
+        last_next = rng.choice([0, 2])  # the last layer: no next layer, or an HBM-resident one
         for step in hist:
             for layer in range(layers):
                 sel = step[layer]
-                lines.append(f"call {layer} {int(layer + 1 < layers)} {k} " + " ".join(map(str, sel)))
-                looked, staged = p.call(layer, sel, layer + 1 < layers)
+                nl = 1 if layer + 1 < layers else last_next
+                # routing weights as float32 values, some tied
+                probs = [float(np.float32(rng.choice([0.5, 1.0, rng.uniform(0.05, 2.5)]))) for _ in sel]
+                lines.append(f"call {layer} {nl} {k} " + " ".join(map(str, sel)) + " " +
+                             " ".join(repr(v) for v in probs))
+                looked, staged = p.call(layer, sel, nl, probs=probs)
                 want.append("L" + "".join(f" {s} {int(c)}" for s, c in looked))
                 want.append("S" + "".join(f" {e} {s}" for e, s in staged))
         want.append("C " + " ".join(str(p.n[c]) for c in COUNTERS))
