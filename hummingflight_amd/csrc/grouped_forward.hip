@@ -51,7 +51,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
+                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.h16, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -87,6 +87,7 @@ int grouped_workspace_alloc() {
         {(void**)&w.xl, 2 * (size_t)T * c.d},
         {(void**)&w.hh, 2 * R * c.I},
         {(void**)&w.hl, 2 * R * c.I},
+        {(void**)&w.h16, 2 * R * c.I},
         {(void**)&w.y, 4 * R * c.d},
         {(void**)&w.part, 4 * tks * c.E},
     };
@@ -183,6 +184,10 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
+    // Prefill tiles: h also as FP16, which the down projection multiplies as
+    // one half (against FP16-converted weights) unless a value overflowed.
+    gu.h_f16 = TR == kPrefillTileRows ? w.h16 : nullptr;
+    gu.h_f16_bad = w.lo_flag + 1;
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
 
@@ -208,6 +213,8 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
+    dn.a_f16 = gu.h_f16;
+    dn.a_f16_bad = w.lo_flag + 1;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;

@@ -46,11 +46,27 @@
 namespace hf {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __fp16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int GBN = 128, GBK = kGemmTileK;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ f16x8_t as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8_t, v); }
+
+// Eight BF16 weights as FP16: widened to FP32 (exact), then packed with
+// round-toward-zero, which is exact too for every BF16 value of FP16's normal
+// range (8 significand bits into 11); smaller ones keep FP16's subnormal
+// spacing (6e-8).
+__device__ __forceinline__ f16x8_t bf16x8_to_f16x8(u32x4 v) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v[i] << 16),
+                                                                         __uint_as_float(v[i] & 0xFFFF0000u)));
+    return __builtin_bit_cast(f16x8_t, r);
+}
 
 // 16-byte load through a global-address-space pointer.  Pointers read from
 // memory (the expert table) are generic; a generic load is a FLAT instruction,
@@ -150,11 +166,13 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
     if (EPI == EPI_SWIGLU) {
         uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
         uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
+        uint16_t* frow = a.h_f16 ? a.h_f16 + (size_t)gr * a.N : nullptr;
+        bool bad = false;
 #pragma unroll
         for (int cb = 0; cb < NCB / 2; ++cb) {
             const int col = col0 + 16 * cb;
             if (col >= a.N) continue;  // N is a multiple of 64: 4 columns all in or all out
-            uint32_t hw[2], lw[2];
+            uint32_t hw[2], lw[2], fw[2];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float gv = acc[cb][q];
@@ -162,17 +180,24 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                 const float hv = gv / (1.0f + expf(-gv)) * uv;
                 const uint32_t hb = f32_to_bf16(hv);
                 const uint32_t lb = f32_to_bf16(hv - __uint_as_float(hb << 16));
+                const _Float16 hf = (_Float16)hv;  // round to nearest even
+                const uint32_t fb = __builtin_bit_cast(uint16_t, hf);
+                bad |= (fb & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
                 if (q & 1) {
                     hw[q >> 1] |= hb << 16;
                     lw[q >> 1] |= lb << 16;
+                    fw[q >> 1] |= fb << 16;
                 } else {
                     hw[q >> 1] = hb;
                     lw[q >> 1] = lb;
+                    fw[q >> 1] = fb;
                 }
             }
             *reinterpret_cast<uint2*>(hrow + col) = make_uint2(hw[0], hw[1]);
             *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
+            if (frow) *reinterpret_cast<uint2*>(frow + col) = make_uint2(fw[0], fw[1]);
         }
+        if (frow && bad) atomicOr(a.h_f16_bad, 1u);
     } else {
         float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
                                          : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
@@ -467,8 +492,11 @@ static_assert(split_lds_max(192, 4) <= 160 * 1024 && split_lds_max(192, 6) <= 16
                   split_lds_max(256, 4) <= 160 * 1024,
               "LDS");
 
-template <int EPI, int ROWS, int HALVES>
+// F16: A is the FP16 copy (a_f16, one half) and the weights are converted to
+// FP16 as they leave the LDS.
+template <int EPI, int ROWS, int HALVES, bool F16 = false>
 __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave) {
+    static_assert(!F16 || HALVES == 1, "the FP16 activations have one half");
     constexpr int CB = split_cb<EPI, ROWS>();
     constexpr int RBW = ROWS / 32;                 // row blocks per wavefront
     constexpr int AST = ROWS * GBK;                // elements per A stage
@@ -547,7 +575,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     auto issue_a = [&](int j) {  // A half of sub-step j
         uint16_t* dst = aring + ((j % RA + RA) % RA) * AST + wave * NAD * 512;
         j = min(max(j, 0), nj - 1);
-        const uint16_t* src = a.a_hi + (j % HALVES ? lo_off : 0) + (j / HALVES) * GBK;
+        const uint16_t* src = (F16 ? a.a_f16 : a.a_hi) + (j % HALVES ? lo_off : 0) + (j / HALVES) * GBK;
 #pragma unroll
         for (int i = 0; i < NAD; ++i) dma16<0>(src + aoff[i], dst + i * 512);
     };
@@ -567,22 +595,32 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     auto compute = [&](const uint16_t* at, const uint16_t* bt) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-            bf16x8_t w[CB];
+            u32x4 w[CB];
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
                 const int r = brow(cb);
                 const int c = (kh * 4 + fq) ^ (r & 7);
-                w[cb] = as_bf16x8(*reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8));
+                w[cb] = *reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8);
+            }
+            [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
+            if constexpr (F16) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[cb]);
             }
 #pragma unroll
             for (int j = 0; j < RBW; ++j) {
                 if (j < nmine) {  // a guard, not a break: acc must stay in registers
                     const int r = 16 * (2 * j + par) + fr;
                     const int c = (kh * 4 + fq) ^ (r & 7);
-                    const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4*>(at + r * GBK + c * 8));
+                    const u32x4 av = *reinterpret_cast<const u32x4*>(at + r * GBK + c * 8);
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb)
-                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[cb], av, acc[j][cb], 0, 0, 0);
+                    for (int cb = 0; cb < CB; ++cb) {
+                        if constexpr (F16)
+                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av), acc[j][cb], 0, 0, 0);
+                        else
+                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[cb]), as_bf16x8(av),
+                                                                                 acc[j][cb], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -658,8 +696,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
+    const bool use_f16 = EPI == EPI_SCATTER && a.a_f16 && *a.a_f16_bad == 0u;
     auto run = [&](int item) {
         if (group_absent(a, a.tile_group ? a.tile_group[item / a.ksplit / a.n_tiles] : 0)) return;
+        if constexpr (EPI == EPI_SCATTER) {
+            if (use_f16) {
+                gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave);
+                __syncthreads();
+                return;
+            }
+        }
         if (LOM != kLoNone && use_lo)
             gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
         else
@@ -833,7 +879,9 @@ hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d,
 
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s) {
-    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 1);
+    // flag[0]: x has a nonzero lo half (set below); flag[1]: an FP16 copy of h
+    // overflowed (set by the gate/up epilogue of the same forward).
+    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 2);
     if (e != hipSuccess) return e;
     size_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;

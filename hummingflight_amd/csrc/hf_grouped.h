@@ -58,6 +58,15 @@ struct GemmArgs {
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
     unsigned* item_ctr;         // 8 zeroed per-XCD work counters (null: static items; see run_items_dynamic)
+    // FP16 activations (the down projection's h, prefill tiles): multiplied
+    // instead of a_hi / a_lo while *a_f16_bad == 0, against the weights
+    // converted to FP16 in registers.
+    const uint16_t* a_f16;
+    const unsigned* a_f16_bad;
+    // SWIGLU: h also as FP16 rows [rows][N] (when not null); *h_f16_bad is set
+    // when a value does not fit FP16 (then the consumer uses the hi / lo halves).
+    uint16_t* h_f16;
+    unsigned* h_f16_bad;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.

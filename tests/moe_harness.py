@@ -39,15 +39,15 @@ class Run:
     """One configured layer on the device plus its oracle twin."""
 
     def __init__(self, dims, n_group=1, topk_group=1, seed=1, T=1, layer=0, n_shared=1,
-                 on_host=False, with_norm=False, bias=None, max_tokens=None, **routing):
+                 on_host=False, with_norm=False, bias=None, max_tokens=None, w_std=0.02, **routing):
         # routing: norm_topk_prob / routed_scaling_factor, passed to both sides
         self.shape = synth.LayerShape(n_group=n_group, topk_group=topk_group, n_shared=n_shared,
                                       **dims, **routing)
         capi.call("hfmoe_configure", self.shape.config(max_tokens=max_tokens or T))
         self.dev = synth.DeviceLayer(self.shape, layer=layer, seed=seed, experts_on_host=on_host,
-                                     with_norm=with_norm, bias=bias)
+                                     with_norm=with_norm, bias=bias, w_std=w_std)
         self.spec = O.LayerSpec(n_group=n_group, topk_group=topk_group, n_shared=n_shared, seed=seed,
-                                layer=layer, bias_override=bias, **dims, **routing)
+                                layer=layer, bias_override=bias, w_std=w_std, **dims, **routing)
         self.ref = O.SyntheticLayer(self.spec)
         self.T = T
         self.layer = layer
