@@ -184,12 +184,21 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
-    // Prefill tiles: h also as FP16, which the down projection multiplies as
-    // one half (against FP16-converted weights) unless a value overflowed.
+    // Prefill tiles: h as FP16, which the down projection multiplies as one
+    // half (against FP16-converted weights).  Should any value not fit FP16,
+    // a second pass (which otherwise exits at once) writes the BF16 hi / lo
+    // halves for the down projection to take instead.
     gu.h_f16 = TR == kPrefillTileRows ? w.h16 : nullptr;
     gu.h_f16_bad = w.lo_flag + 1;
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
+    if (gu.h_f16) {
+        GemmArgs hl = gu;
+        hl.h_f16 = nullptr;
+        hl.run_if = gu.h_f16_bad;
+        hl.item_ctr = nullptr;  // the counters are spent: static items
+        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, hl, gemm_blocks(TR), s), "gate/up hi/lo gemm");
+    }
 
     // Down projections of every group; row r's output lands at row perm[r] of
     // y: pair slot t*k + r for routed rows, T*k + t for the shared expert.

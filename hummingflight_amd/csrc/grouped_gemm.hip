@@ -98,6 +98,22 @@ __device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* l) {
                                      (__attribute__((address_space(3))) void*)l, 16, 0, POLICY);
 }
 
+// The same DMA through a raw buffer resource (buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes at base + voff + soff (bytes) land at l + 16 l bytes.
+// Unlike the FLAT-encoded global_load_lds, which the compiler must assume
+// may still be writing LDS when an LDS read's wait is placed (it then waits
+// for every LDS read with lgkmcnt(0)), a buffer DMA leaves the compiler free
+// to wait for just the read it needs, so LDS reads can run ahead of the
+// multiplies that use them.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+    // stride 0, 4 GiB of records, 32-bit data format (untyped loads)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+template <int POLICY = kDmaPolicy>
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint16_t* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)l, 16, voff, soff, 0, POLICY);
+}
+
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -110,6 +126,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the asm statements keep the compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Barrier that also makes this wavefront's LDS writes visible (lgkmcnt(0)
+// first), still without waiting for global loads or stores.
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7, lgkmcnt 0
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
@@ -156,17 +181,20 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
 
 // Stores one lane's share of a finished tile row gr: acc[cb][q] is output
 // column col0 + 16*cb + q (q = 0..3).  SWIGLU: blocks [0, NCB/2) are gate and
-// [NCB/2, NCB) the matching up columns; writes h = silu(g) * u as BF16 hi/lo
-// (glm_forward.cpp:444-446), 8 bytes each.  PARTIAL / SCATTER: 16-byte FP32
-// stores (row stride N is a multiple of 4 whenever N is a multiple of 64;
-// a ragged router width falls back to single floats).
-template <int EPI, int NCB>
+// [NCB/2, NCB) the matching up columns; writes h = silu(g) * u
+// (glm_forward.cpp:444-446), 8 bytes per array: as FP16 alone when a.h_f16 is
+// given (setting *a.h_f16_bad when a value does not fit FP16), else as BF16
+// hi/lo.  PARTIAL / SCATTER: 16-byte FP32 stores (row stride N is a multiple
+// of 4 whenever N is a multiple of 64; a ragged router width falls back to
+// single floats) to output row orow_idx (SCATTER: the token-order row of gr;
+// PARTIAL: gr).  NT: non-temporal stores.
+template <int EPI, int NCB, bool NT = false>
 __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t (&acc)[NCB], int gr, int col0,
-                                               int ks) {
+                                               int ks, int orow_idx) {
     if (EPI == EPI_SWIGLU) {
+        uint16_t* frow = a.h_f16 ? a.h_f16 + (size_t)gr * a.N : nullptr;
         uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
         uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
-        uint16_t* frow = a.h_f16 ? a.h_f16 + (size_t)gr * a.N : nullptr;
         bool bad = false;
 #pragma unroll
         for (int cb = 0; cb < NCB / 2; ++cb) {
@@ -177,36 +205,48 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
             for (int q = 0; q < 4; ++q) {
                 const float gv = acc[cb][q];
                 const float uv = acc[cb + NCB / 2][q];
-                const float hv = gv / (1.0f + expf(-gv)) * uv;
-                const uint32_t hb = f32_to_bf16(hv);
-                const uint32_t lb = f32_to_bf16(hv - __uint_as_float(hb << 16));
-                const _Float16 hf = (_Float16)hv;  // round to nearest even
-                const uint32_t fb = __builtin_bit_cast(uint16_t, hf);
-                bad |= (fb & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
-                if (q & 1) {
-                    hw[q >> 1] |= hb << 16;
-                    lw[q >> 1] |= lb << 16;
-                    fw[q >> 1] |= fb << 16;
+                // The hardware exp2 and reciprocal (a few ulp of FP32): far
+                // below the rounding of h to FP16 or to a BF16 hi + lo pair.
+                const float hv = __fdividef(gv, 1.0f + __expf(-gv)) * uv;
+                uint32_t v0, v1 = 0;
+                if (frow) {
+                    const _Float16 hf = (_Float16)hv;  // round to nearest even
+                    v0 = __builtin_bit_cast(uint16_t, hf);
+                    bad |= (v0 & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
                 } else {
-                    hw[q >> 1] = hb;
-                    lw[q >> 1] = lb;
-                    fw[q >> 1] = fb;
+                    v0 = f32_to_bf16(hv);
+                    v1 = f32_to_bf16(hv - __uint_as_float(v0 << 16));
+                }
+                if (q & 1) {
+                    fw[q >> 1] |= v0 << 16;
+                    hw[q >> 1] |= v0 << 16;
+                    lw[q >> 1] |= v1 << 16;
+                } else {
+                    fw[q >> 1] = v0;
+                    hw[q >> 1] = v0;
+                    lw[q >> 1] = v1;
                 }
             }
-            *reinterpret_cast<uint2*>(hrow + col) = make_uint2(hw[0], hw[1]);
-            *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
-            if (frow) *reinterpret_cast<uint2*>(frow + col) = make_uint2(fw[0], fw[1]);
+            if (frow) {
+                *reinterpret_cast<uint2*>(frow + col) = make_uint2(fw[0], fw[1]);
+            } else {
+                *reinterpret_cast<uint2*>(hrow + col) = make_uint2(hw[0], hw[1]);
+                *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
+            }
         }
         if (frow && bad) atomicOr(a.h_f16_bad, 1u);
     } else {
-        float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + gr) * a.N
-                                         : a.out_f32 + (size_t)a.scatter_rows[gr] * a.N;
+        float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + orow_idx) * a.N
+                                         : a.out_f32 + (size_t)orow_idx * a.N;
         const bool vec = (a.N & 3) == 0;
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) {
             const int col = col0 + 16 * cb;
             if (vec && col + 3 < a.N) {
-                *reinterpret_cast<f32x4_t*>(orow + col) = acc[cb];
+                if constexpr (NT)
+                    __builtin_nontemporal_store(acc[cb], reinterpret_cast<f32x4_t*>(orow + col));
+                else
+                    *reinterpret_cast<f32x4_t*>(orow + col) = acc[cb];
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
@@ -399,7 +439,9 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, int item, BStage* r
     for (int rb = 0; rb < 2; ++rb) {
         if (rb >= nrb) break;
         const int rl = 32 * wave + 16 * rb + fr;
-        if (rl < rows) store_tile_row<EPI, 8>(a, acc[rb], row0 + rl, n0 + 4 * fq, ks);
+        if (rl < rows)
+            store_tile_row<EPI, 8>(a, acc[rb], row0 + rl, n0 + 4 * fq, ks,
+                                   EPI == EPI_SCATTER ? a.scatter_rows[row0 + rl] : row0 + rl);
     }
 }
 
@@ -420,6 +462,7 @@ __device__ __forceinline__ bool group_absent(const GemmArgs& a, int g) {
 template <int EPI, int LOM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) BStage ring[];  // kRingBytes
+    if (a.run_if && *a.run_if == 0u) return;
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar branches
 
@@ -494,8 +537,11 @@ static_assert(split_lds_max(192, 4) <= 160 * 1024 && split_lds_max(192, 6) <= 16
 
 // F16: A is the FP16 copy (a_f16, one half) and the weights are converted to
 // FP16 as they leave the LDS.
-template <int EPI, int ROWS, int HALVES, bool F16 = false>
-__device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave) {
+// on_setup() runs once the item's own loads (tile table, row map) are out,
+// before its first DMA.
+template <int EPI, int ROWS, int HALVES, bool F16 = false, class Setup>
+__device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
+                                                Setup&& on_setup) {
     static_assert(!F16 || HALVES == 1, "the FP16 activations have one half");
     constexpr int CB = split_cb<EPI, ROWS>();
     constexpr int RBW = ROWS / 32;                 // row blocks per wavefront
@@ -538,18 +584,25 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     const int kbase = ks * Kc;
 
     // DMA slot i (16 bytes) of a stage holds chunk (i & 7) ^ (r & 7) of stage
-    // row r = i >> 3.  Activation rows past the tile's end re-read its last
-    // row.  Weight rows: SWIGLU rows [0, 32 CB) are gate rows n0.., the next
+    // row r = i >> 3.  Activation DMA j of a wavefront fills the 8-row block
+    // 8 j + wave (the blocks spread over the wavefronts); rows past the tile's
+    // end re-read its last row, and with SKIP_A the blocks past its last
+    // 16-row block, which nothing multiplies, are not loaded at all: an
+    // activation DMA takes a slot of the memory pipeline's queue even when it
+    // hits in L1, and near-uniform prefill fills a 192-row tile to ~128 rows.
+    // Weight rows: SWIGLU rows [0, 32 CB) are gate rows n0.., the next
     // 32 CB the matching up rows; a wavefront's 8 CB slot rows lie in one half.
+    constexpr bool SKIP_A = split_a_may_skip(HALVES, DA, DB, NAD, NBD);
+    const int nab = 2 * nrb;
     uint32_t aoff[NAD], boff[NBD];
 #pragma unroll
     for (int j = 0; j < NAD; ++j) {
-        const int i = (wave * NAD + j) * 64 + lane;
+        const int i = (j * 8 + wave) * 64 + lane;
         const int r = i >> 3;
         const int c = (i & 7) ^ (r & 7);
         const int gr = row0 + min(r, rows - 1);
         const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
-        aoff[j] = (uint32_t)(src * a.K + kbase + c * 8);
+        aoff[j] = (uint32_t)(2 * (src * a.K + kbase + c * 8));
     }
 #pragma unroll
     for (int j = 0; j < NBD; ++j) {
@@ -558,10 +611,13 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         const int c = (i & 7) ^ (r & 7);
         int n = EPI == EPI_SWIGLU ? n0 + r % (32 * CB) : n0 + r;
         n = min(n, a.N - 1);
-        boff[j] = (uint32_t)((size_t)n * a.b_ld + kbase + c * 8);
+        boff[j] = (uint32_t)(2 * ((size_t)n * a.b_ld + kbase + c * 8));
     }
-    const uint16_t* bbase = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
-    const ptrdiff_t lo_off = HALVES == 2 ? a.a_lo - a.a_hi : 0;
+    // Byte offsets within 4 GiB of each operand's base (every activation and
+    // weight buffer of a layer is far smaller).
+    const __amdgpu_buffer_rsrc_t rb = raw_rsrc((EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0);
+    const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(F16 ? a.a_f16 : a.a_hi);
+    const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
 
     f32x4_t acc[RBW][CB];
 #pragma unroll
@@ -570,20 +626,23 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         for (int cb = 0; cb < CB; ++cb) acc[j][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
     // Sub-step / stage indices outside [0, nj) / [0, nk) (prologue and tail)
-    // load the nearest valid one into the slot of the index itself: a slot
-    // that nothing reads before its own stage lands there, in issue order.
+    // load nothing.  The prologue's are issued before every real load, so no
+    // wait count includes them; the waits that could count a missing tail
+    // load wait for everything instead (substep).
     auto issue_a = [&](int j) {  // A half of sub-step j
-        uint16_t* dst = aring + ((j % RA + RA) % RA) * AST + wave * NAD * 512;
-        j = min(max(j, 0), nj - 1);
-        const uint16_t* src = (F16 ? a.a_f16 : a.a_hi) + (j % HALVES ? lo_off : 0) + (j / HALVES) * GBK;
+        if (j < 0 || j >= nj) return;
+        uint16_t* dst = aring + (j % RA) * AST;
+        const __amdgpu_buffer_rsrc_t ra = j % HALVES ? ra1 : ra0;
+        const uint32_t soff = (uint32_t)(j / HALVES) * (2 * GBK);
 #pragma unroll
-        for (int i = 0; i < NAD; ++i) dma16<0>(src + aoff[i], dst + i * 512);
+        for (int i = 0; i < NAD; ++i)
+            if (!SKIP_A || i * 8 + wave < nab) dma16<0>(ra, aoff[i], soff, dst + (i * 8 + wave) * 512);
     };
     auto issue_b = [&](int s) {  // B of K stage s
-        uint16_t* dst = bring + ((s % RB + RB) % RB) * (64 * CB * GBK) + wave * NBD * 512;
-        s = min(max(s, 0), nk - 1);
+        if (s < 0 || s >= nk) return;
+        uint16_t* dst = bring + (s % RB) * (64 * CB * GBK) + wave * NBD * 512;
 #pragma unroll
-        for (int i = 0; i < NBD; ++i) dma16(bbase + boff[i] + s * GBK, dst + i * 512);
+        for (int i = 0; i < NBD; ++i) dma16(rb, boff[i], (uint32_t)s * (2 * GBK), dst + i * 512);
     };
     // B stage row of this wavefront's column block cb.  The weights are the
     // MFMA's first operand, so lane (fr, fq) ends with output columns
@@ -592,34 +651,64 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         return EPI == EPI_SWIGLU ? (cb < CB / 2 ? 8 * CB * cg + 16 * cb : 32 * CB + 8 * CB * cg + 16 * (cb - CB / 2)) + fr
                                  : 16 * CB * cg + 16 * cb + fr;
     };
+    // LDS fragments: weights of column block cb, activations of row block j,
+    // K half kh of the stage.
+    auto wfrag = [&](const uint16_t* bt, int cb, int kh) {
+        const int r = brow(cb);
+        const int c = (kh * 4 + fq) ^ (r & 7);
+        return *reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8);
+    };
+    auto afrag = [&](const uint16_t* at, int j, int kh) {
+        const int r = 16 * (2 * j + par) + fr;
+        const int c = (kh * 4 + fq) ^ (r & 7);
+        return *reinterpret_cast<const u32x4*>(at + r * GBK + c * 8);
+    };
+    // One stage's multiplies as a chain of steps (kh, j), j < nmine, each
+    // reading the next step's activation fragment before its own multiplies
+    // so that the LDS latency hides under them.  Every step's fragment has a
+    // variable of its own (av[kh][j], all indices compile-time), so no copy
+    // has to wait for a read in flight.  Per accumulator the order of the
+    // multiplies is kh = 0 then 1, as ever.
     auto compute = [&](const uint16_t* at, const uint16_t* bt) {
+        u32x4 w[2][CB];
+        u32x4 av[2][RBW];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
+        av[0][0] = afrag(at, 0, 0);
+        constexpr bool W1_EARLY = RBW * CB <= 24;  // registers permitting (not 384 columns or 256 rows)
+        if constexpr (W1_EARLY) {  // kh = 1's weights now too
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
+        }
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-            u32x4 w[CB];
+            if constexpr (!W1_EARLY) {
+                if (kh == 1) {
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const int r = brow(cb);
-                const int c = (kh * 4 + fq) ^ (r & 7);
-                w[cb] = *reinterpret_cast<const u32x4*>(bt + r * GBK + c * 8);
+                    for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
+                }
             }
             [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
             if constexpr (F16) {
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[cb]);
+                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[kh][cb]);
             }
 #pragma unroll
             for (int j = 0; j < RBW; ++j) {
                 if (j < nmine) {  // a guard, not a break: acc must stay in registers
-                    const int r = 16 * (2 * j + par) + fr;
-                    const int c = (kh * 4 + fq) ^ (r & 7);
-                    const u32x4 av = *reinterpret_cast<const u32x4*>(at + r * GBK + c * 8);
+                    if (j + 1 < nmine) {
+                        if (j + 1 < RBW) av[kh][j + 1] = afrag(at, j + 1, kh);
+                    } else if (kh == 0) {
+                        av[1][0] = afrag(at, 0, 1);
+                    }
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
                         if constexpr (F16)
-                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av), acc[j][cb], 0, 0, 0);
+                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av[kh][j]), acc[j][cb],
+                                                                                0, 0, 0);
                         else
-                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[cb]), as_bf16x8(av),
-                                                                                 acc[j][cb], 0, 0, 0);
+                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]),
+                                                                                 as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
                     }
                 }
             }
@@ -628,15 +717,35 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     auto substep = [&](int s, auto half_c) {
         constexpr int half = decltype(half_c)::value;
         const int j = s * HALVES + half;
-        wait_vmcnt<split_after(HALVES, DA, DB, half, NAD, NBD)>();
+        // The loads issued before this sub-step go up to A(j - 1 + DA) and
+        // B(floor((j - 1) / H) + DB): while all exist the steady count holds.
+        const int jp = j - 1;
+        const int sp = (jp >= 0 ? jp : jp - (HALVES - 1)) / HALVES;  // floor
+        if (jp + DA < nj && sp + DB < nk)
+            wait_vmcnt<split_after(HALVES, DA, DB, half, NAD, NBD)>();
+        else
+            wait_vmcnt<0>();
         lds_barrier();
         issue_a(j + DA);
         if (half == 0) issue_b(s + DB);
         compute(aring + (j % RA) * AST, bring + (s % RB) * (64 * CB * GBK));
     };
+    // SCATTER: the token-order output rows of the epilogue, read now (192-row
+    // tiles; the 256-row tiles have no registers to spare) so that their
+    // latency hides under the item.
+    constexpr bool EARLY_ROWS = EPI == EPI_SCATTER && ROWS == kPrefillTileRows;
+    [[maybe_unused]] int orow[EARLY_ROWS ? RBW : 1];
+    if constexpr (EARLY_ROWS) {
+#pragma unroll
+        for (int j = 0; j < RBW; ++j) {
+            const int rl = 16 * (2 * j + par) + fr;
+            orow[j] = j < nmine && rl < rows ? a.scatter_rows[row0 + rl] : 0;
+        }
+    }
+    on_setup();
     // Prologue: the sub-steps before 0 of the steady pattern (ops with an
-    // index below 0 load stage 0 into the slot of that index), so the counts
-    // split_after assumes hold from sub-step 0 on.
+    // index below 0 load nothing), so the counts split_after assumes hold
+    // from sub-step 0 on.
     constexpr int Q = DA > HALVES * DB ? DA : HALVES * DB;
 #pragma unroll
     for (int q = -Q; q < 0; ++q) {
@@ -648,74 +757,100 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         if constexpr (HALVES == 2) substep(s, std::integral_constant<int, 1>{});
     }
 
+    // Every load of the item has landed (the last sub-steps wait for all).
+    // Epilogue: the output rows (SCATTER: y, read once by the combine) go out
+    // with non-temporal stores.
 #pragma unroll
     for (int j = 0; j < RBW; ++j) {
         const int rl = 16 * (2 * j + par) + fr;
         const int col0 = EPI == EPI_SWIGLU ? n0 + 8 * CB * cg + 4 * fq : n0 + 16 * CB * cg + 4 * fq;
-        if (j < nmine && rl < rows) store_tile_row<EPI, CB>(a, acc[j], row0 + rl, col0, ks);
+        if (j < nmine && rl < rows) {
+            int dst = row0 + rl;
+            if constexpr (EARLY_ROWS)
+                dst = orow[j];
+            else if (EPI == EPI_SCATTER)
+                dst = a.scatter_rows[row0 + rl];
+            store_tile_row<EPI, CB, EPI == EPI_SCATTER>(a, acc[j], row0 + rl, col0, ks, dst);
+        }
     }
 }
 
 // Dynamic items of the prefill kernel: each XCD's workgroups take the items of
 // the XCD's M tiles in order from a counter (zeroed by the dispatch), then help
 // the other XCDs with theirs, so the kernel ends when the last item does, not
-// when the workgroup dealt the most items does.  Every grab advances a counter
-// and each counter stops yielding at its XCD's item count: the loop ends.
+// when the workgroup dealt the most items does.  Thread 0 takes the next item
+// while the current one runs (its atomic goes out with the item's first
+// loads), so no workgroup waits on the counter between items.  Every grab
+// advances a counter and each counter stops yielding at its XCD's item count:
+// the loop ends.
 template <class Run>
 __device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange& r, int m_tiles, Run&& run) {
     const int t = threadIdx.x;
     __shared__ int next_item;
-    int probe = 0;
-    for (;;) {
-        if (t == 0) {
-            int got = -1;
-            while (got < 0 && probe < r.nxcd) {
-                const int x = (r.xcd + probe) % r.nxcd;
-                const int li = (int)atomicAdd(a.item_ctr + x, 1u);
-                const int n = (m_tiles - x + r.nxcd - 1) / r.nxcd * r.per_m;
-                if (li < n)
-                    got = (x + r.nxcd * (li / r.per_m)) * r.per_m + li % r.per_m;
-                else
-                    ++probe;
-            }
-            next_item = got;
+    int probe = 0;  // thread 0: counters found spent, in probing order from this XCD's
+    auto grab = [&]() { return (int)atomicAdd(a.item_ctr + (r.xcd + probe) % r.nxcd, 1u); };
+    // Thread 0: the item of grab li, probing the next counters once one is spent; -1 when all are.
+    auto settle = [&](int li) {
+        for (;;) {
+            const int x = (r.xcd + probe) % r.nxcd;
+            if (li < (m_tiles - x + r.nxcd - 1) / r.nxcd * r.per_m)
+                return (x + r.nxcd * (li / r.per_m)) * r.per_m + li % r.per_m;
+            if (++probe >= r.nxcd) return -1;
+            li = grab();
         }
-        __syncthreads();
-        const int item = next_item;
-        __syncthreads();
-        if (item < 0) break;
-        run(item);
+    };
+    auto publish = [&](int v) {  // thread 0's value to the workgroup
+        if (t == 0) next_item = v;
+        lds_sync();
+        v = next_item;
+        lds_sync();
+        return v;
+    };
+    int item = publish(t == 0 ? settle(grab()) : 0);
+    while (item >= 0) {
+        int li = 0;
+        run(item, [&] {
+            if (t == 0 && probe < r.nxcd) li = grab();
+        });
+        item = publish(t == 0 ? (probe < r.nxcd ? settle(li) : -1) : 0);
     }
 }
 
 template <int EPI, int LOM, int ROWS>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t slds[];  // split_lds_max(ROWS, CB) bytes
+    if (a.run_if && *a.run_if == 0u) return;
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
     const bool use_f16 = EPI == EPI_SCATTER && a.a_f16 && *a.a_f16_bad == 0u;
-    auto run = [&](int item) {
-        if (group_absent(a, a.tile_group ? a.tile_group[item / a.ksplit / a.n_tiles] : 0)) return;
+    // One item, then a barrier: every wavefront is done with the LDS rings
+    // before the next item's loads land in them.  (The item's own loads have
+    // all landed; its stores need not have.)
+    auto run = [&](int item, auto&& on_setup) {
+        if (group_absent(a, a.tile_group ? a.tile_group[item / a.ksplit / a.n_tiles] : 0)) {
+            on_setup();
+            return;
+        }
         if constexpr (EPI == EPI_SCATTER) {
             if (use_f16) {
-                gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave);
-                __syncthreads();
+                gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave, on_setup);
+                lds_barrier();
                 return;
             }
         }
         if (LOM != kLoNone && use_lo)
-            gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave);
+            gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave, on_setup);
         else
-            gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave);
-        __syncthreads();
+            gemm_item_split<EPI, ROWS, 1>(a, item, slds, t, wave, on_setup);
+        lds_barrier();
     };
     // 256-row tiles fill the whole 160 KB of LDS, leaving none for the
     // dynamic loop's shared item slot: they always take static items.
     if (ROWS != kPrefillTileRows || !a.item_ctr || !r.by_mtile) {
-        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li));
+        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li), [] {});
         return;
     }
     if constexpr (ROWS == kPrefillTileRows) dynamic_items(a, r, m_tiles, run);

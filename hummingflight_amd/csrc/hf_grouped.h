@@ -63,10 +63,15 @@ struct GemmArgs {
     // converted to FP16 in registers.
     const uint16_t* a_f16;
     const unsigned* a_f16_bad;
-    // SWIGLU: h also as FP16 rows [rows][N] (when not null); *h_f16_bad is set
-    // when a value does not fit FP16 (then the consumer uses the hi / lo halves).
+    // SWIGLU: h as FP16 rows [rows][N] instead of the hi / lo halves (when not
+    // null); *h_f16_bad is set when a value does not fit FP16 (then the
+    // consumer needs the hi / lo halves: see run_if).
     uint16_t* h_f16;
     unsigned* h_f16_bad;
+    // When not null, the launch does nothing unless *run_if != 0 (a second
+    // gate/up pass that writes the BF16 hi / lo halves only after some h did
+    // not fit FP16).
+    const unsigned* run_if;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.

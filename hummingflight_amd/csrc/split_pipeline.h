@@ -47,4 +47,13 @@ constexpr int split_after(int H, int DA, int DB, int half, int NAD, int NBD) {
     return n;
 }
 
+// True when no wait count includes A instructions: then a wavefront may issue
+// fewer than NAD per A stage (the tile's unused rows) and every wait still
+// covers the loads it guards.
+constexpr bool split_a_may_skip(int H, int DA, int DB, int NAD, int NBD) {
+    for (int half = 0; half < H; ++half)
+        if (split_after(H, DA, DB, half, NAD, NBD) != split_after(H, DA, DB, half, 0, NBD)) return false;
+    return true;
+}
+
 }  // namespace hf

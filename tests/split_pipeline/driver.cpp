@@ -1,6 +1,6 @@
 // Prints the prefill GEMM pipeline parameters (split_pipeline.h) for every
 // configuration the library instantiates: rows swiglu halves cb da db nad nbd
-// after_half0 after_half1 lds_bytes.
+// after_half0 after_half1 lds_bytes a_may_skip.
 #include <cstdio>
 
 #include "split_pipeline.h"
@@ -14,9 +14,9 @@ int main() {
                 const int cb = split_cb(swiglu != 0, rows);
                 const int da = split_da(rows, cb, h), db = split_db(rows, cb, h);
                 const int nad = rows / 64, nbd = cb;
-                std::printf("%d %d %d %d %d %d %d %d %d %d %zu\n", rows, swiglu, h, cb, da, db, nad, nbd,
+                std::printf("%d %d %d %d %d %d %d %d %d %d %zu %d\n", rows, swiglu, h, cb, da, db, nad, nbd,
                             split_after(h, da, db, 0, nad, nbd), h == 2 ? split_after(h, da, db, 1, nad, nbd) : -1,
-                            split_lds_max(rows, cb));
+                            split_lds_max(rows, cb), split_a_may_skip(h, da, db, nad, nbd) ? 1 : 0);
             }
     return 0;
 }
