@@ -70,9 +70,10 @@ void prof_end(Pending& p, hipStream_t s) {
     if (!launched) {  // nothing was launched in the section
         g.event_pool.push_back(p.start);
         g.event_pool.push_back(p.stop);
-        return;
+    } else {
+        g.pending.push_back(p);
     }
-    g.pending.push_back(p);
+    p.name = nullptr;  // ended: a second prof_end is a no-op
 }
 
 void prof_drain() {

@@ -561,6 +561,11 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     const int nk = Kc / GBK;
     const int nj = nk * HALVES;
 
+    // The item comes through LDS on the dynamic path: make it (and all that
+    // derives from it: tile, rows, the row-block guards) provably uniform, so
+    // that its loads are scalar and its guards scalar branches rather than
+    // exec-mask juggling on every multiply of the K loop.
+    item = __builtin_amdgcn_readfirstlane(item);
     const int ks = item % a.ksplit;
     const int rest = item / a.ksplit;
     const int nt = rest % a.n_tiles;
@@ -629,14 +634,14 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // load nothing.  The prologue's are issued before every real load, so no
     // wait count includes them; the waits that could count a missing tail
     // load wait for everything instead (substep).
-    auto issue_a = [&](int j) {  // A half of sub-step j
+    auto issue_a = [&](int j, int nab_s) {  // A half of sub-step j
         if (j < 0 || j >= nj) return;
         uint16_t* dst = aring + (j % RA) * AST;
         const __amdgpu_buffer_rsrc_t ra = j % HALVES ? ra1 : ra0;
         const uint32_t soff = (uint32_t)(j / HALVES) * (2 * GBK);
 #pragma unroll
         for (int i = 0; i < NAD; ++i)
-            if (!SKIP_A || i * 8 + wave < nab) dma16<0>(ra, aoff[i], soff, dst + (i * 8 + wave) * 512);
+            if (!SKIP_A || i * 8 + wave < nab_s) dma16<0>(ra, aoff[i], soff, dst + (i * 8 + wave) * 512);
     };
     auto issue_b = [&](int s) {  // B of K stage s
         if (s < 0 || s >= nk) return;
@@ -669,7 +674,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // variable of its own (av[kh][j], all indices compile-time), so no copy
     // has to wait for a read in flight.  Per accumulator the order of the
     // multiplies is kh = 0 then 1, as ever.
-    auto compute = [&](const uint16_t* at, const uint16_t* bt) {
+    auto compute = [&](const uint16_t* at, const uint16_t* bt, int nm) {
         u32x4 w[2][CB];
         u32x4 av[2][RBW];
 #pragma unroll
@@ -695,8 +700,8 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
             }
 #pragma unroll
             for (int j = 0; j < RBW; ++j) {
-                if (j < nmine) {  // a guard, not a break: acc must stay in registers
-                    if (j + 1 < nmine) {
+                if (j < nm) {  // a guard, not a break: acc must stay in registers
+                    if (j + 1 < nm) {
                         if (j + 1 < RBW) av[kh][j + 1] = afrag(at, j + 1, kh);
                     } else if (kh == 0) {
                         av[1][0] = afrag(at, 0, 1);
@@ -726,9 +731,14 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         else
             wait_vmcnt<0>();
         lds_barrier();
-        issue_a(j + DA);
+        // Fresh scalar copies of the item's bounds in every sub-step: the
+        // compiler would otherwise hoist each guard's comparison out of the K
+        // loop as a lane mask and rebuild a branch from it at every guard.
+        int nm = nmine, nab_s = nab;
+        asm volatile("" : "+s"(nm), "+s"(nab_s));
+        issue_a(j + DA, nab_s);
         if (half == 0) issue_b(s + DB);
-        compute(aring + (j % RA) * AST, bring + (s % RB) * (64 * CB * GBK));
+        compute(aring + (j % RA) * AST, bring + (s % RB) * (64 * CB * GBK), nm);
     };
     // SCATTER: the token-order output rows of the epilogue, read now (192-row
     // tiles; the 256-row tiles have no registers to spare) so that their
@@ -749,7 +759,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     constexpr int Q = DA > HALVES * DB ? DA : HALVES * DB;
 #pragma unroll
     for (int q = -Q; q < 0; ++q) {
-        issue_a(q + DA);
+        issue_a(q + DA, nab);
         if ((q % HALVES) == 0) issue_b(q / HALVES + DB);
     }
     for (int s = 0; s < nk; ++s) {
