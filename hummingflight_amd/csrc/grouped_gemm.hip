@@ -1007,6 +1007,14 @@ static hipError_t launch_epi(const GemmArgs& a, int blocks, hipStream_t s) {
 }
 
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s) {
+    // The prefill kernel addresses each operand through a buffer resource
+    // with 32-bit byte offsets: every weight matrix and activation array of a
+    // launch must lie within 4 GiB of its base (at most a few hundred MB at
+    // the supported shapes).
+    const size_t lim = (size_t)1 << 32;
+    if (a.tile_rows != kGemmTileRows &&
+        ((size_t)a.N * (size_t)a.b_ld * 2 >= lim || (size_t)a.rows_total * (size_t)a.K * 2 >= lim))
+        return hipErrorInvalidValue;
     switch (epi) {
         case EPI_PARTIAL: return launch_epi<EPI_PARTIAL>(a, blocks, s);
         case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, blocks, s);
