@@ -515,16 +515,14 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(Gem
 // re-reads its weights).  ROWS = 256 for one-group GEMMs (dense layers, LM
 // head), whose weights are re-read once per M tile.
 //
-// What bounds these GEMMs is the rate of memory requests per CU: ~67-77
-// outstanding 128-byte line requests at ~680-730 cycles of average latency,
-// i.e. 12-15 B per cycle, at the ~1.8-2.0 GHz the GPU runs under this MFMA
-// load; activation re-reads (L2 hits) are a third of those requests.  So
-// tiles are as wide as registers and LDS allow: every N tile
-// re-reads its M tile's activations, and the down projection's 384 columns
-// (CB = 6, 144 registers of accumulators per lane) cut those re-reads by a
-// third against 256.  Gate/up keeps 256 weight rows (CB = 4) so that its
-// weights run two stages ahead in the LDS; one stage ahead costs it more than
-// the saved re-reads bring.
+// At T = 4096 the weight stream alone (this kernel's DMA pattern, no
+// multiplies) and the multiplies alone (no DMA) each take about 70 % of the
+// kernel's time: what is lost is their overlap, with one workgroup of eight
+// wavefronts per CU meeting at a barrier every stage.  Tiles are as wide as
+// registers and LDS allow (fewer items, fewer activation re-reads): the down
+// projection's 384 columns (CB = 6, 144 registers of accumulators per lane),
+// and gate/up's 256 weight rows (CB = 4) so that its weights run two stages
+// ahead in the LDS; one stage ahead costs it more than wider tiles bring.
 //
 // The lo half of A runs as its own sub-step against the same B stage, so an
 // A stage is always one half (ROWS x 64 BF16).  Depths, ring sizes and wait
