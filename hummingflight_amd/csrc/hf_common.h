@@ -128,8 +128,11 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 }
 
 // Weight loads that stream through the cache hierarchy once.
+// Through a global (not generic) pointer: a generic one compiles to a FLAT
+// load, which counts in both vmcnt and lgkmcnt, so every wait for it becomes
+// vmcnt(0) lgkmcnt(0) and no load can stay in flight across a wait.
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
-    return __builtin_nontemporal_load(p);
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)p);
 }
 
 __device__ __forceinline__ u32x4 ld_plain(const u32x4* p) { return *p; }
