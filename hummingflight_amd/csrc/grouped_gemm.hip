@@ -109,9 +109,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
     // stride 0, 4 GiB of records, 32-bit data format (untyped loads)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
 }
+// A wavefront-uniform pointer moved into scalar registers.  A pointer read
+// from memory the kernel also writes (the expert table) comes back from a
+// vector load; a buffer resource built from it would sit in vector registers
+// and every buffer instruction on it would run as a loop over its distinct
+// values (readfirstlane, compare, exec mask) -- once, but at a dozen
+// instructions per DMA.
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
 template <int POLICY = kDmaPolicy>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint16_t* l) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)l, 16, voff, soff, 0, POLICY);
+}
+
+// f(integral_constant<int, i>) for i = N, N - 1, ..., 1.
+template <int N, class F>
+__device__ __forceinline__ void static_for_desc(F&& f) {
+    if constexpr (N > 0) {
+        f(std::integral_constant<int, N>{});
+        static_for_desc<N - 1>(f);
+    }
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
@@ -618,7 +640,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     }
     // Byte offsets within 4 GiB of each operand's base (every activation and
     // weight buffer of a layer is far smaller).
-    const __amdgpu_buffer_rsrc_t rb = raw_rsrc((EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0);
+    const __amdgpu_buffer_rsrc_t rb = raw_rsrc(uniform_ptr((EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0));
     const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(F16 ? a.a_f16 : a.a_hi);
     const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
 
@@ -672,9 +694,14 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // variable of its own (av[kh][j], all indices compile-time), so no copy
     // has to wait for a read in flight.  Per accumulator the order of the
     // multiplies is kh = 0 then 1, as ever.
-    auto compute = [&](const uint16_t* at, const uint16_t* bt, int nm) {
+    // One stage's multiplies for a wavefront with NM row blocks, as straight
+    // code: a guard per row block inside the K loop becomes a branch per
+    // block, and the counter waits at the branches' joins fall back to
+    // lgkmcnt(0), which serialises every fragment read with its multiplies.
+    auto compute_n = [&](const uint16_t* at, const uint16_t* bt, auto nm_c) {
+        constexpr int NM = decltype(nm_c)::value;
         u32x4 w[2][CB];
-        u32x4 av[2][RBW];
+        u32x4 av[2][NM];
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
         av[0][0] = afrag(at, 0, 0);
@@ -690,6 +717,44 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
                 }
+            }
+            [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
+            if constexpr (F16) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[kh][cb]);
+            }
+#pragma unroll
+            for (int j = 0; j < NM; ++j) {
+                if (j + 1 < NM)
+                    av[kh][j + 1] = afrag(at, j + 1, kh);
+                else if (kh == 0)
+                    av[1][0] = afrag(at, 0, 1);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    if constexpr (F16)
+                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av[kh][j]), acc[j][cb],
+                                                                            0, 0, 0);
+                    else
+                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]),
+                                                                             as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // The same with the row-block count known only at run time (a guard per
+    // row block): for tiles whose accumulators leave no registers for a K
+    // loop per row-block count (384 columns, or 256 rows).
+    auto compute_rt = [&](const uint16_t* at, const uint16_t* bt, int nm) {
+        u32x4 w[2][CB];
+        u32x4 av[2][RBW];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
+        av[0][0] = afrag(at, 0, 0);
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            if (kh == 1) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
             }
             [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
             if constexpr (F16) {
@@ -717,7 +782,10 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
             }
         }
     };
-    auto substep = [&](int s, auto half_c) {
+    // One K loop per row-block count where registers allow it (192-row
+    // gate/up tiles: 96 accumulator registers), else one K loop with guards.
+    constexpr bool PER_NM = RBW * CB <= 24;
+    auto substep = [&](int s, auto half_c, auto nm_c) {
         constexpr int half = decltype(half_c)::value;
         const int j = s * HALVES + half;
         // The loads issued before this sub-step go up to A(j - 1 + DA) and
@@ -736,7 +804,12 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         asm volatile("" : "+s"(nm), "+s"(nab_s));
         issue_a(j + DA, nab_s);
         if (half == 0) issue_b(s + DB);
-        compute(aring + (j % RA) * AST, bring + (s % RB) * (64 * CB * GBK), nm);
+        const uint16_t* at = aring + (j % RA) * AST;
+        const uint16_t* bt = bring + (s % RB) * (64 * CB * GBK);
+        if constexpr (!PER_NM)
+            compute_rt(at, bt, nm);
+        else if constexpr (decltype(nm_c)::value > 0)
+            compute_n(at, bt, nm_c);
     };
     // SCATTER: the token-order output rows of the epilogue, read now (192-row
     // tiles; the 256-row tiles have no registers to spare) so that their
@@ -760,9 +833,21 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         issue_a(q + DA, nab);
         if ((q % HALVES) == 0) issue_b(q / HALVES + DB);
     }
-    for (int s = 0; s < nk; ++s) {
-        substep(s, std::integral_constant<int, 0>{});
-        if constexpr (HALVES == 2) substep(s, std::integral_constant<int, 1>{});
+    // The K loop, compiled once per row-block count of the wavefront (0 ..
+    // RBW) and chosen once per item, so each stage's multiplies are straight
+    // code with exact counter waits.
+    auto kloop = [&](auto nm_c) {
+        for (int s = 0; s < nk; ++s) {
+            substep(s, std::integral_constant<int, 0>{}, nm_c);
+            if constexpr (HALVES == 2) substep(s, std::integral_constant<int, 1>{}, nm_c);
+        }
+    };
+    if constexpr (PER_NM) {
+        static_for_desc<RBW + 1>([&](auto n1_c) {
+            if (nmine == decltype(n1_c)::value - 1) kloop(std::integral_constant<int, decltype(n1_c)::value - 1>{});
+        });
+    } else {
+        kloop(std::integral_constant<int, -1>{});
     }
 
     // Every load of the item has landed (the last sub-steps wait for all).
