@@ -383,29 +383,21 @@ def run_lm_head(args) -> dict:
     return res
 
 
-def prefill_tiles(shape: synth.LayerShape, T: int) -> bool:
-    """The library's switch to the 192-row prefill tiles (experts average 96+ rows)."""
-    return T * shape.top_k >= 96 * shape.n_experts
-
-
 def grouped_algorithmic(shape: synth.LayerShape, T: int, U: int) -> dict[str, tuple[int, int]]:
     """(bytes, flops) each multi-token kernel must move / compute at least once.
 
     U = distinct routed experts hit by the batch; the shared expert is one more
     group in the same GEMM launches.  Weights are read once per launch,
-    activations once per token (x as BF16 [T, d]).  The SwiGLU intermediate h
-    and the expert outputs y are counted in the form the kernels exchange them:
-    with prefill tiles h and y as FP16 (2 bytes per element), otherwise h as a
-    BF16 hi + lo pair (4 bytes) and y as FP32.
+    activations once per token (x as BF16 [T, d]), the SwiGLU intermediate
+    counted at 4 bytes per element, expert outputs as FP32.
     """
     d, I, E, k, S = shape.hidden, shape.inter, shape.n_experts, shape.top_k, shape.n_shared
     R = T * k + S * T  # GEMM rows: routed (token, rank) pairs + shared-expert rows
-    hb, yb = (2, 2) if prefill_tiles(shape, T) else (4, 4)
     return {
         "router_gemm": (E * d * 2 + T * d * 2 + T * E * 4, 2 * T * E * d),
-        "expert_gateup_gemm": ((U + S) * 2 * I * d * 2 + T * d * 2 + R * I * hb, 2 * R * 2 * I * d),
-        "expert_down_gemm": ((U + S) * d * I * 2 + R * I * hb + R * d * yb, 2 * R * d * I),
-        "combine": (R * d * yb + T * k * 4 + T * d * 4, 2 * T * k * d),
+        "expert_gateup_gemm": ((U + S) * 2 * I * d * 2 + T * d * 2 + R * I * 4, 2 * R * 2 * I * d),
+        "expert_down_gemm": ((U + S) * d * I * 2 + R * I * 4 + R * d * 4, 2 * R * d * I),
+        "combine": (R * d * 4 + T * k * 4 + T * d * 4, 2 * T * k * d),
     }
 
 

@@ -51,7 +51,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.h16, w.y, w.y16, w.part};
+                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.h16, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -89,7 +89,6 @@ int grouped_workspace_alloc() {
         {(void**)&w.hl, 2 * R * c.I},
         {(void**)&w.h16, 2 * R * c.I},
         {(void**)&w.y, 4 * R * c.d},
-        {(void**)&w.y16, 2 * R * c.d},
         {(void**)&w.part, 4 * tks * c.E},
     };
     for (auto& a : list) {
@@ -153,7 +152,7 @@ int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     return HFMOE_OK;
 }
 
-int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s, bool y16_ok) {
+int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     const Cfg& c = g.cfg;
     GroupedWorkspace& w = g.gws;
     const int P = T * c.k;
@@ -225,33 +224,17 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s, bool y16_
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
     dn.a_f16 = gu.h_f16;
     dn.a_f16_bad = w.lo_flag + 1;
-    // Prefill tiles: y as FP16 (half the bytes written here and read by the
-    // combine); should any value not fit FP16, a second pass (which otherwise
-    // exits at once) writes the FP32 y for the combine to take instead.
-    dn.out_f16 = TR == kPrefillTileRows && y16_ok && c.d % 8 == 0 ? w.y16 : nullptr;
-    dn.out_f16_bad = w.lo_flag + 2;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
-    if (dn.out_f16) {
-        GemmArgs d32 = dn;
-        d32.out_f16 = nullptr;
-        d32.run_if = dn.out_f16_bad;
-        d32.item_ctr = nullptr;  // the counters are spent: static items
-        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, d32, gemm_blocks(TR), s), "down gemm (FP32 y)");
-    }
     return HFMOE_OK;
 }
 
-int grouped_combine(int T, float* out, hipStream_t s, bool y16) {
+int grouped_combine(int T, float* out, hipStream_t s) {
     const Cfg& c = g.cfg;
     const int P = T * c.k;
-    // The same condition as the down projection's FP16 y (grouped_experts).
-    const bool f16 = y16 && expert_tile_rows(T) == kPrefillTileRows && c.d % 8 == 0;
     Pending p;
     prof_begin(p, "combine", s);
-    HF_CHECK_LAUNCH(launch_combine(g.ws.wts, g.gws.y, f16 ? g.gws.y16 : nullptr, g.gws.lo_flag + 2, T, c.k, c.d,
-                                   c.n_shared > 0 ? P : -1, out, s),
-                    "combine");
+    HF_CHECK_LAUNCH(launch_combine(g.ws.wts, g.gws.y, T, c.k, c.d, c.n_shared > 0 ? P : -1, out, s), "combine");
     return HFMOE_OK;
 }
 
@@ -259,8 +242,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
                     const hfmoe_route_debug* dbg) {
     if (!g.gws.xh) return forward_tokenwise(L, x, T, out, s, dbg);
     int rc = grouped_route(L, x, T, s);
-    if (!rc) rc = grouped_experts(L.dev.etab, T, s, true);
-    if (!rc) rc = grouped_combine(T, out, s, true);
+    if (!rc) rc = grouped_experts(L.dev.etab, T, s);
+    if (!rc) rc = grouped_combine(T, out, s);
     return rc ? rc : copy_debug(dbg, T, s);
 }
 

@@ -278,56 +278,6 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
     }
 }
 
-// One finished row of a prefill down-projection tile (split kernel): acc[2c]
-// and acc[2c + 1] hold the output columns col0 + 32 c + 0..3 and + 4..7 (the
-// interleaved column pairs of gemm_item_split), stored to y row orow_idx with
-// non-temporal stores (y is read once, by the combine): as FP16 when
-// a.out_f16 is given (returns true when a value does not fit FP16), else as
-// FP32.  Columns past N (a ragged last tile) are not stored.
-template <int NCB>
-__device__ __forceinline__ bool store_scatter_pairs(const GemmArgs& a, const f32x4_t (&acc)[NCB], int col0,
-                                                    int orow_idx) {
-    static_assert(NCB % 2 == 0, "column blocks come in pairs");
-    bool bad = false;
-#pragma unroll
-    for (int c = 0; c < NCB / 2; ++c) {
-        const int col = col0 + 32 * c;
-        const float v[8] = {acc[2 * c][0],     acc[2 * c][1],     acc[2 * c][2],     acc[2 * c][3],
-                            acc[2 * c + 1][0], acc[2 * c + 1][1], acc[2 * c + 1][2], acc[2 * c + 1][3]};
-        if (a.out_f16) {
-            uint16_t* orow = a.out_f16 + (size_t)orow_idx * a.N;
-            uint32_t w[4];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v[q]);  // round to nearest even
-                bad |= (h & 0x7C00u) == 0x7C00u;                                 // inf or NaN: does not fit FP16
-                if (q & 1)
-                    w[q >> 1] |= h << 16;
-                else
-                    w[q >> 1] = h;
-            }
-            if (col + 7 < a.N) {
-                __builtin_nontemporal_store((u32x4){w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4*>(orow + col));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    if (col + q < a.N) orow[col + q] = (uint16_t)(w[q >> 1] >> (16 * (q & 1)));
-            }
-        } else {
-            float* orow = a.out_f32 + (size_t)orow_idx * a.N;
-            if (col + 7 < a.N) {
-                __builtin_nontemporal_store(acc[2 * c], reinterpret_cast<f32x4_t*>(orow + col));
-                __builtin_nontemporal_store(acc[2 * c + 1], reinterpret_cast<f32x4_t*>(orow + col + 4));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    if (col + q < a.N) orow[col + q] = v[q];
-            }
-        }
-    }
-    return bad;
-}
-
 // One (m-tile, n-tile, k-split) item.  USE_LO: multiply the A lo half too.
 //
 // Pipeline per K stage s (64 k), prefetch distance D: every wave waits until
@@ -722,18 +672,9 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // B stage row of this wavefront's column block cb.  The weights are the
     // MFMA's first operand, so lane (fr, fq) ends with output columns
     // 4 fq .. 4 fq + 3 of the block for row fr of the row block.
-    // SCATTER: column blocks 2c and 2c + 1 interleave their MFMA rows (row m
-    // of block 2c + e is weight row 32 c + 8 (m / 4) + 4 e + m % 4 of the
-    // wavefront's group), so that lane (fr, fq) ends with the 8 consecutive
-    // output columns 32 c + 8 fq .. + 7 of each pair: one 16-byte store per
-    // pair (FP16 y) or two adjacent ones (FP32).
     auto brow = [&](int cb) {
-        if constexpr (EPI == EPI_SWIGLU)
-            return (cb < CB / 2 ? 8 * CB * cg + 16 * cb : 32 * CB + 8 * CB * cg + 16 * (cb - CB / 2)) + fr;
-        else if constexpr (EPI == EPI_SCATTER)
-            return 16 * CB * cg + 32 * (cb >> 1) + 8 * (fr >> 2) + 4 * (cb & 1) + (fr & 3);
-        else
-            return 16 * CB * cg + 16 * cb + fr;
+        return EPI == EPI_SWIGLU ? (cb < CB / 2 ? 8 * CB * cg + 16 * cb : 32 * CB + 8 * CB * cg + 16 * (cb - CB / 2)) + fr
+                                 : 16 * CB * cg + 16 * cb + fr;
     };
     // LDS fragments: weights of column block cb, activations of row block j,
     // K half kh of the stage.
@@ -912,22 +853,18 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // Every load of the item has landed (the last sub-steps wait for all).
     // Epilogue: the output rows (SCATTER: y, read once by the combine) go out
     // with non-temporal stores.
-    [[maybe_unused]] bool bad = false;
 #pragma unroll
     for (int j = 0; j < RBW; ++j) {
         const int rl = 16 * (2 * j + par) + fr;
+        const int col0 = EPI == EPI_SWIGLU ? n0 + 8 * CB * cg + 4 * fq : n0 + 16 * CB * cg + 4 * fq;
         if (j < nmine && rl < rows) {
-            if constexpr (EPI == EPI_SCATTER) {
-                const int dst = EARLY_ROWS ? orow[j] : a.scatter_rows[row0 + rl];
-                bad |= store_scatter_pairs<CB>(a, acc[j], n0 + 16 * CB * cg + 8 * fq, dst);
-            } else {
-                const int col0 = EPI == EPI_SWIGLU ? n0 + 8 * CB * cg + 4 * fq : n0 + 16 * CB * cg + 4 * fq;
-                store_tile_row<EPI, CB>(a, acc[j], row0 + rl, col0, ks, row0 + rl);
-            }
+            int dst = row0 + rl;
+            if constexpr (EARLY_ROWS)
+                dst = orow[j];
+            else if (EPI == EPI_SCATTER)
+                dst = a.scatter_rows[row0 + rl];
+            store_tile_row<EPI, CB, EPI == EPI_SCATTER>(a, acc[j], row0 + rl, col0, ks, dst);
         }
-    }
-    if constexpr (EPI == EPI_SCATTER) {
-        if (bad) atomicOr(a.out_f16_bad, 1u);
     }
 }
 
@@ -1039,46 +976,6 @@ __global__ void combine_kernel(const float* __restrict__ wts, const float* __res
         m.w += v.w;
     }
     reinterpret_cast<float4*>(out)[i4] = m;
-}
-
-// The same merge over y as FP16 (eight columns per thread), or over the FP32
-// y when *y16_bad says the FP16 copy overflowed (then a second down-projection
-// pass wrote it): one launch either way, the choice made on the device.
-__device__ __forceinline__ void add8(float (&m)[8], float w, const u32x4 v) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const uint16_t h = (uint16_t)(v[q >> 1] >> (16 * (q & 1)));
-        m[q] += w * (float)__builtin_bit_cast(_Float16, h);
-    }
-}
-__global__ void combine_f16_kernel(const float* __restrict__ wts, const float* __restrict__ y,
-                                   const uint16_t* __restrict__ y16, const unsigned* __restrict__ y16_bad, int T,
-                                   int k, int d, int shared_row0, float* __restrict__ out) {
-    const size_t i8 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int d8 = d >> 3;
-    if (i8 >= (size_t)T * d8) return;
-    const int t = (int)(i8 / d8), n8 = (int)(i8 % d8);
-    float m[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    if (*y16_bad == 0u) {
-        const u32x4* yv = reinterpret_cast<const u32x4*>(y16);
-        for (int r = 0; r < k; ++r)
-            add8(m, wts[(size_t)t * k + r], __builtin_nontemporal_load(yv + ((size_t)t * k + r) * d8 + n8));
-        if (shared_row0 >= 0) add8(m, 1.0f, __builtin_nontemporal_load(yv + ((size_t)shared_row0 + t) * d8 + n8));
-    } else {
-        const f32x4_t* y4 = reinterpret_cast<const f32x4_t*>(y);
-        auto add = [&](float w, size_t row) {
-            const f32x4_t a = __builtin_nontemporal_load(y4 + row * (2 * d8) + 2 * n8);
-            const f32x4_t b = __builtin_nontemporal_load(y4 + row * (2 * d8) + 2 * n8 + 1);
-            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int q = 0; q < 8; ++q) m[q] += w * v[q];
-        };
-        for (int r = 0; r < k; ++r) add(wts[(size_t)t * k + r], (size_t)t * k + r);
-        if (shared_row0 >= 0) add(1.0f, (size_t)shared_row0 + t);
-    }
-    float4* o = reinterpret_cast<float4*>(out) + 2 * i8;
-    o[0] = make_float4(m[0], m[1], m[2], m[3]);
-    o[1] = make_float4(m[4], m[5], m[6], m[7]);
 }
 
 // x FP32 [n] -> BF16 hi/lo; *flag |= 1 when any lo is nonzero.  Eight values
@@ -1209,14 +1106,9 @@ hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream
     }
 }
 
-hipError_t launch_combine(const float* wts, const float* y, const uint16_t* y16, const unsigned* y16_bad, int T,
-                          int k, int d, int shared_row0, float* out, hipStream_t s) {
+hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d, int shared_row0,
+                          float* out, hipStream_t s) {
     const size_t n4 = (size_t)T * (d / 4);
-    if (y16 && d % 8 == 0) {
-        const size_t n8 = (size_t)T * (d / 8);
-        return launch(combine_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, wts, y, y16, y16_bad,
-                      T, k, d, shared_row0, out);
-    }
     return launch(combine_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, wts, y, T, k, d,
                   shared_row0, out);
 }
@@ -1224,9 +1116,8 @@ hipError_t launch_combine(const float* wts, const float* y, const uint16_t* y16,
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s) {
     // flag[0]: x has a nonzero lo half (set below); flag[1]: an FP16 copy of h
-    // overflowed (set by the gate/up epilogue of the same forward); flag[2]: an
-    // FP16 copy of y overflowed (set by the down projection).
-    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 3);
+    // overflowed (set by the gate/up epilogue of the same forward).
+    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 2);
     if (e != hipSuccess) return e;
     size_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;

@@ -48,7 +48,6 @@ struct GroupedWorkspace {
     uint16_t* hl = nullptr;      // [rows, I] h lo
     uint16_t* h16 = nullptr;     // [rows, I] h as FP16 (prefill down projection)
     float* y = nullptr;          // [rows, d] expert outputs at pair slots, shared rows after
-    uint16_t* y16 = nullptr;     // [rows, d] the same as FP16 (prefill tiles)
     float* part = nullptr;       // [ksplit, maxT, E] router split-K partials
     int max_tiles = 0;
 };
@@ -200,11 +199,8 @@ int forward_grouped(LayerState& L, const float* x, int T, float* out, hipStream_
 // gate/up and down GEMMs of the groups whose etab entries are not null (3 per
 // group, E + 1 groups, the shared expert last), and the weighted combine.
 int grouped_route(LayerState& L, const float* x, int T, hipStream_t s);
-// y16_ok: the expert outputs of this call are combined on their own (not
-// across several calls, as the streamed waves are), so prefill tiles may
-// write them as FP16 (with an FP32 pass only after an FP16 overflow).
-int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s, bool y16_ok);
-int grouped_combine(int T, float* out, hipStream_t s, bool y16);
+int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s);
+int grouped_combine(int T, float* out, hipStream_t s);
 int grouped_tile_rows(int T);
 int grouped_workspace_alloc();
 void grouped_workspace_free();

@@ -72,11 +72,6 @@ struct GemmArgs {
     // gate/up pass that writes the BF16 hi / lo halves only after some h did
     // not fit FP16).
     const unsigned* run_if;
-    // SCATTER, prefill tiles: y as FP16 rows [rows][N] instead of out_f32
-    // (when not null); *out_f16_bad is set when a value does not fit FP16
-    // (then a second pass, run_if = out_f16_bad, writes out_f32).
-    uint16_t* out_f16;
-    unsigned* out_f16_bad;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.
@@ -86,9 +81,8 @@ hipError_t launch_clear_u32(unsigned* p, int n, hipStream_t s);
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s);
 // out[t] = sum_r wts[t, r] * y[t*k + r] (+ y[shared_row0 + t] when shared_row0 >= 0); d % 4 == 0.
-// With y16 (d % 8 == 0): y is read from the FP16 copy y16 unless *y16_bad.
-hipError_t launch_combine(const float* wts, const float* y, const uint16_t* y16, const unsigned* y16_bad, int T,
-                          int k, int d, int shared_row0, float* out, hipStream_t s);
+hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d, int shared_row0,
+                          float* out, hipStream_t s);
 hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, const float* bias,
                                 float* logits, float2* scores, hipStream_t s);
 // Stable counting sort of the T*k (token, rank) pairs by expert plus the M-tile

@@ -341,7 +341,7 @@ int streamed_forward_batch(int layer, LayerState& L, const float* x, int T, floa
         if (e == hipSuccess && wv > 0 && dynamic_items)  // the dispatch zeroed them for the first wave
             e = launch_clear_u32(g.gws.item_ctr, kItemCounters, s);
         if (e != hipSuccess) return fail_hip(e, "wave table upload");
-        rc = grouped_experts(L.etab_dev, T, s, false);
+        rc = grouped_experts(L.etab_dev, T, s);
         if (rc) return rc;
         for (int slot : claimed) {
             e = hipEventRecord(P.consumed[slot], s);
@@ -356,7 +356,7 @@ int streamed_forward_batch(int layer, LayerState& L, const float* x, int T, floa
         if (rc) return rc;
         claimed.push_back(slot);
     }
-    rc = grouped_combine(T, out, s, false);
+    rc = grouped_combine(T, out, s);
     return rc ? rc : copy_debug(dbg, T, s);
 }
 
