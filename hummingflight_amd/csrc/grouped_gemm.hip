@@ -214,49 +214,60 @@ template <int EPI, int NCB, bool NT = false>
 __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t (&acc)[NCB], int gr, int col0,
                                                int ks, int orow_idx) {
     if (EPI == EPI_SWIGLU) {
-        uint16_t* frow = a.h_f16 ? a.h_f16 + (size_t)gr * a.N : nullptr;
-        uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
-        uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
-        bool bad = false;
+        // h = silu(g) * u with the hardware exp2 and reciprocal (a few ulp of
+        // FP32): far below the rounding of h to FP16 or to a BF16 hi + lo pair.
+        float hv[NCB / 2][4];
 #pragma unroll
-        for (int cb = 0; cb < NCB / 2; ++cb) {
-            const int col = col0 + 16 * cb;
-            if (col >= a.N) continue;  // N is a multiple of 64: 4 columns all in or all out
-            uint32_t hw[2], lw[2], fw[2];
+        for (int cb = 0; cb < NCB / 2; ++cb)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float gv = acc[cb][q];
-                const float uv = acc[cb + NCB / 2][q];
-                // The hardware exp2 and reciprocal (a few ulp of FP32): far
-                // below the rounding of h to FP16 or to a BF16 hi + lo pair.
-                const float hv = __fdividef(gv, 1.0f + __expf(-gv)) * uv;
-                uint32_t v0, v1 = 0;
-                if (frow) {
-                    const _Float16 hf = (_Float16)hv;  // round to nearest even
-                    v0 = __builtin_bit_cast(uint16_t, hf);
-                    bad |= (v0 & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
-                } else {
-                    v0 = f32_to_bf16(hv);
-                    v1 = f32_to_bf16(hv - __uint_as_float(v0 << 16));
-                }
-                if (q & 1) {
-                    fw[q >> 1] |= v0 << 16;
-                    hw[q >> 1] |= v0 << 16;
-                    lw[q >> 1] |= v1 << 16;
-                } else {
-                    fw[q >> 1] = v0;
-                    hw[q >> 1] = v0;
-                    lw[q >> 1] = v1;
-                }
+                hv[cb][q] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[cb + NCB / 2][q];
             }
-            if (frow) {
+        bool bad = false;
+        if (a.h_f16) {  // FP16 h, one 8-byte store per column block
+            uint16_t* frow = a.h_f16 + (size_t)gr * a.N;
+#pragma unroll
+            for (int cb = 0; cb < NCB / 2; ++cb) {
+                const int col = col0 + 16 * cb;
+                if (col >= a.N) continue;  // N is a multiple of 64: 4 columns all in or all out
+                uint32_t fw[2];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t v0 = __builtin_bit_cast(uint16_t, (_Float16)hv[cb][q]);  // round to nearest even
+                    bad |= (v0 & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
+                    if (q & 1)
+                        fw[q >> 1] |= v0 << 16;
+                    else
+                        fw[q >> 1] = v0;
+                }
                 *reinterpret_cast<uint2*>(frow + col) = make_uint2(fw[0], fw[1]);
-            } else {
+            }
+        } else {  // BF16 hi + lo halves
+            uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
+            uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
+#pragma unroll
+            for (int cb = 0; cb < NCB / 2; ++cb) {
+                const int col = col0 + 16 * cb;
+                if (col >= a.N) continue;
+                uint32_t hw[2], lw[2];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t v0 = f32_to_bf16(hv[cb][q]);
+                    const uint32_t v1 = f32_to_bf16(hv[cb][q] - __uint_as_float(v0 << 16));
+                    if (q & 1) {
+                        hw[q >> 1] |= v0 << 16;
+                        lw[q >> 1] |= v1 << 16;
+                    } else {
+                        hw[q >> 1] = v0;
+                        lw[q >> 1] = v1;
+                    }
+                }
                 *reinterpret_cast<uint2*>(hrow + col) = make_uint2(hw[0], hw[1]);
                 *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
             }
         }
-        if (frow && bad) atomicOr(a.h_f16_bad, 1u);
+        if (bad) atomicOr(a.h_f16_bad, 1u);
     } else {
         float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + orow_idx) * a.N
                                          : a.out_f32 + (size_t)orow_idx * a.N;
