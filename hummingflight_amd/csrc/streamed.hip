@@ -124,15 +124,20 @@ static int pool_init() {
 }
 
 // Queues expert eid's [gate | up | down] (host) into slot on the copy stream,
-// after the last kernel that read the slot.
+// after the last kernel that read the slot: one copy of the whole expert when
+// its three matrices lie back to back in host memory (the reference's expert
+// block, uploaded with one copy, cuda_backend.cpp:416-418), else one per matrix.
 static int copy_expert(const LayerState& L, int eid, int slot) {
     StreamPool& P = g.pool;
     const size_t proj = (size_t)g.cfg.I * g.cfg.d;
     uint16_t* dst = P.base + (size_t)slot * (P.slot_bytes / 2);
+    const uint16_t* const* m = &L.host_experts[3 * (size_t)eid];
     hipError_t e = hipStreamWaitEvent(g.copy_stream, P.consumed[slot], 0);
-    for (int q = 0; q < 3 && e == hipSuccess; ++q)
-        e = hipMemcpyAsync(dst + q * proj, L.host_experts[3 * eid + q], proj * 2, hipMemcpyHostToDevice,
-                           g.copy_stream);
+    if (e == hipSuccess && m[1] == m[0] + proj && m[2] == m[1] + proj)
+        e = hipMemcpyAsync(dst, m[0], 3 * proj * 2, hipMemcpyHostToDevice, g.copy_stream);
+    else
+        for (int q = 0; q < 3 && e == hipSuccess; ++q)
+            e = hipMemcpyAsync(dst + q * proj, m[q], proj * 2, hipMemcpyHostToDevice, g.copy_stream);
     if (e == hipSuccess) e = hipEventRecord(P.copied[slot], g.copy_stream);
     if (e != hipSuccess) return fail_hip(e, "expert H2D");
     g.pcie_bytes += 3 * proj * 2;
