@@ -103,6 +103,7 @@ _SIGS = [
     ("hfmoe_moe_forward_debug", C.c_int,
      [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(RouteDebug)]),
     ("hfmoe_moe_forward_noalloc", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
+    ("hfmoe_moe_forward_bf16", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     ("hfmoe_moe_layer", C.c_int, [C.c_int, C.c_void_p, C.c_void_p]),
     ("hfmoe_mlp_block", C.c_int, [C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
     ("hfmoe_register_dense_layer", C.c_int, [C.c_int, C.POINTER(DenseWeights)]),

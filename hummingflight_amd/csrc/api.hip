@@ -402,6 +402,22 @@ int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out
     return forward_grouped(L, x_dev, T, out_dev, s, dbg);
 }
 
+int hfmoe_moe_forward_bf16(int layer, const uint16_t* x_dev, int32_t T, float* out_dev, void* stream) {
+    int rc = require_cfg();
+    if (rc) return rc;
+    if (T < 0 || T > g.max_tokens)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "T=%d outside 0..max_tokens=%d", T, g.max_tokens);
+    if (T == 0) return HFMOE_OK;
+    if (!x_dev) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null activation pointer");
+    if (reinterpret_cast<uintptr_t>(x_dev) & 15) return fail(HFMOE_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (!g.ws.tmp) return fail(HFMOE_ERR_NOT_INITIALIZED, "workspace is not allocated");
+    // x widened to FP32 (exactly) in the workspace's [max_tokens, d] scratch
+    // rows, then the FP32 forward on the same stream.
+    hipError_t e = launch_bf16_to_f32(x_dev, g.ws.tmp, (size_t)T * g.cfg.d, pick_stream(stream));
+    if (e != hipSuccess) return fail_hip(e, "x BF16 -> FP32");
+    return hfmoe_moe_forward_debug(layer, g.ws.tmp, T, out_dev, stream, nullptr);
+}
+
 int hfmoe_moe_layer(int layer, const float* input_host, float* output_host) {
     int rc = require_cfg();
     if (rc) return rc;

@@ -26,7 +26,7 @@ struct Workspace {
     float* out_io = nullptr;     // [d]
     float* io_pin = nullptr;     // pinned host [2, d], coherent: the host contract's x, then out
     float* io_pin_dev = nullptr; // its device address (null: copies go through hipMemcpyAsync)
-    float* tmp = nullptr;        // [2, maxT, d] (mlp block: normed x, MoE out)
+    float* tmp = nullptr;        // [2, maxT, d] (mlp block: normed x, MoE out; BF16 x widened)
 };
 
 // Buffers of the multi-token (dispatch + grouped) path.  Sorted rows: the
@@ -225,6 +225,7 @@ hipError_t launch_rmsnorm(const float* h, const uint16_t* w, float* out, int T, 
                           hipStream_t s);
 hipError_t launch_add_inplace(float* dst, const float* src, size_t n, hipStream_t s);
 hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s);
+hipError_t launch_bf16_to_f32(const uint16_t* src, float* dst, size_t n, hipStream_t s);
 // dst[0, n) = src[0, n) by a kernel (either may be mapped pinned host memory).
 hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, size_t n, hipStream_t s);
 hipError_t launch_copy_u64(const uint64_t* src, uint64_t* dst, size_t n, hipStream_t s);

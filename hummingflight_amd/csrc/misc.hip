@@ -69,6 +69,32 @@ hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s
     return launch(copy_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
 }
 
+// BF16 bits -> FP32 (exact: a BF16 value is the top half of its FP32), eight
+// values per thread and step (a 16-byte load, two 16-byte stores) when both
+// buffers are 16-byte aligned, then single values for the rest.
+__global__ void bf16_to_f32_kernel(const uint16_t* __restrict__ src, float* __restrict__ dst, size_t n) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    const size_t n8 = vec ? n / 8 : 0;
+    for (size_t i = tid; i < n8; i += stride) {
+        const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+        float4* o = reinterpret_cast<float4*>(dst) + 2 * i;
+        o[0] = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16),
+                           __uint_as_float(v.y & 0xFFFF0000u));
+        o[1] = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u), __uint_as_float(v.w << 16),
+                           __uint_as_float(v.w & 0xFFFF0000u));
+    }
+    for (size_t i = n8 * 8 + tid; i < n; i += stride) dst[i] = __uint_as_float((uint32_t)src[i] << 16);
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t* src, float* dst, size_t n, hipStream_t s) {
+    size_t blocks = (n / 8 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    return launch(bf16_to_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+}
+
 __global__ void copy_u32_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, size_t n) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];

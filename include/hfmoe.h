@@ -123,6 +123,12 @@ int hfmoe_moe_forward_debug(int layer, const float* x_dev, int32_t T, float* out
  * shape hfmoe_configure accepts fits.  HBM-resident MoE layers only.  Calls on
  * one GPU share that array: calls that overlap in time on one GPU race. */
 int hfmoe_moe_forward_noalloc(int layer, const float* x_dev, int32_t T, float* out_dev, void* stream);
+/* hfmoe_moe_forward with the activations as BF16 bits [T, hidden] (16-byte
+ * aligned): moeLayer's FP32 input (glm_forward.h:93) held as BF16 by an engine
+ * that keeps its activations in BF16.  x is widened to FP32 exactly, into the
+ * library's scratch rows, and the FP32 forward runs on the same stream: the
+ * output equals hfmoe_moe_forward's on those FP32 values, bit for bit. */
+int hfmoe_moe_forward_bf16(int layer, const uint16_t* x_dev, int32_t T, float* out_dev, void* stream);
 /* The moeLayer contract itself: one token, host FP32 buffers, synchronous. */
 int hfmoe_moe_layer(int layer, const float* input_host, float* output_host);
 /* h_dev[T, hidden] += MLP(RMSNorm(h_dev)) -- the MLP half of a decoder layer

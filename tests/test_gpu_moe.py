@@ -117,6 +117,31 @@ def layer_weights(dev, **override):
     return capi.LayerWeights(f["router"], f["bias"], f["sg"], f["su"], f["sd"], f["experts"], f["norm"], f["loc"], 0)
 
 
+@pytest.mark.parametrize("T", [1, 37, 1024])
+def test_bf16_activations_match_fp32(hf, T):
+    # hfmoe_moe_forward_bf16 takes x as BF16 bits and must give exactly what
+    # hfmoe_moe_forward gives for the same values held as FP32: decode (T = 1),
+    # batched tiles (T = 37) and prefill tiles (T = 1024 over 64 experts).
+    d = SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=95, T=T)
+    x = synth.make_x_dev(T, d, seed=95)
+    bits = (x.download(np.float32, T * d).view(np.uint32) >> 16).astype(np.uint16)
+    xb = capi.DeviceBuffer.of(bits)
+    a = capi.DeviceBuffer(T * d * 4)
+    b = capi.DeviceBuffer(T * d * 4)
+    capi.call("hfmoe_moe_forward", 0, x.ptr, T, a.ptr, None)
+    capi.call("hfmoe_moe_forward_bf16", 0, xb.ptr, T, b.ptr, None)
+    capi.call("hfmoe_synchronize")
+    got, want = b.download(np.float32, T * d), a.download(np.float32, T * d)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # Misaligned x is refused before anything is launched.
+    rc = capi.load().hfmoe_moe_forward_bf16(0, xb.ptr + 2, T, b.ptr, None)
+    assert rc == capi.ERR_INVALID_ARGUMENT
+    for buf in (x, xb, a, b):
+        buf.free()
+    r.free()
+
+
 def test_misaligned_weights_are_rejected(hf):
     # 16-byte vector and LDS-DMA loads read the weights: an 8-byte-aligned view
     # (a safetensors tensor may start at any multiple of 8) is refused at
