@@ -223,6 +223,17 @@ public:
             it = (int)(uint32_t)(it->first >> 32) == layer ? heat_.erase(it) : std::next(it);
     }
 
+    // Empties one slot: the copy meant to fill it was never queued, so the
+    // entry placed there must not be served.  A later lookup copies it again.
+    void drop_slot(int s) {
+        if (s < 0 || s >= slots() || key_[s] == kEmpty) return;
+        where_.erase(key_[s]);
+        unlink(s);
+        key_[s] = kEmpty;
+        protect_[s] = 0;
+        staged_[s] = used_[s] = pinned_[s] = 0;
+    }
+
     // Pin a resident entry: no victim while an unpinned slot can be taken.
     void pin(uint64_t key) {
         const int s = find(key);

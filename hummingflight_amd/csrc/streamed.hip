@@ -139,7 +139,10 @@ static int copy_expert(const LayerState& L, int eid, int slot) {
         for (int q = 0; q < 3 && e == hipSuccess; ++q)
             e = hipMemcpyAsync(dst + q * proj, m[q], proj * 2, hipMemcpyHostToDevice, g.copy_stream);
     if (e == hipSuccess) e = hipEventRecord(P.copied[slot], g.copy_stream);
-    if (e != hipSuccess) return fail_hip(e, "expert H2D");
+    if (e != hipSuccess) {
+        P.policy.drop_slot(slot);  // the slot holds no copy of the expert: never serve it
+        return fail_hip(e, "expert H2D");
+    }
     g.pcie_bytes += 3 * proj * 2;
     return HFMOE_OK;
 }

@@ -8,6 +8,7 @@
 //   call LAYER NEXT K E1 .. EK [P1 .. PK]   (NEXT: 0 no next layer, 1 streamed,
 //        2 HBM-resident; P: the winners' routing weights)
 //   forget LAYER  (the layer was re-registered: drop its cached experts)
+//   drop SLOT     (the copy into SLOT failed: the slot becomes empty)
 // stdout per call: "L s0 c0 s1 c1 ..." (slot, copy flag per selected expert),
 // then "S e0 s0 e1 s1 ..." (copied-ahead expert and slot); at the end the
 // counters in the order of hfmoe_stream_counters.
@@ -42,6 +43,10 @@ int main() {
             }
             p.opt.prefetch = pf != 0;
             p.opt.ema_predictor = ema != 0;
+        } else if (cmd == "drop") {
+            int slot = -1;
+            in >> slot;
+            p.drop_slot(slot);
         } else if (cmd == "forget") {
             int layer = 0;
             in >> layer;

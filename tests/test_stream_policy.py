@@ -237,3 +237,16 @@ def test_library_forget_layer_drops_only_that_layer(driver):
     assert out[4] == "L 0 1 1 1"  # layer 0 copied again into its freed slots
     assert out[6] == "L 2 0 3 0"  # layer 1 still resident
     assert out[-1].split()[1:4] == ["8", "2", "6"]  # lookups, hits, misses
+
+
+def test_library_drop_slot_recopies(driver):
+    # A copy that could not be queued leaves its slot empty: the next lookup of
+    # that expert copies it again instead of serving a slot that never received
+    # it (no counterpart in the reference, whose staging either succeeds or
+    # falls back to the CPU).
+    lines = ["opt 0 0 0.1 0.5 0.5", "reset 4", "call 0 0 2 5 6", "drop 1", "call 0 0 2 5 6", "drop 9", "drop -1"]
+    r = subprocess.run([driver], input="\n".join(lines) + "\n", capture_output=True, text=True, check=True)
+    out = r.stdout.strip().split("\n")
+    assert out[0] == "L 0 1 1 1"
+    assert out[2] == "L 0 0 1 1"  # expert 5 still resident, expert 6 copied again into the freed slot
+    assert out[-1].split()[1:4] == ["4", "1", "3"]  # lookups, hits, misses
