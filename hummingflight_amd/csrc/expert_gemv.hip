@@ -9,8 +9,8 @@
 //            (2*d BF16, 16-byte coalesced loads) against x staged in LDS as
 //            FP32, writes h[slot][i] = silu(g)*u in FP32.  Shared-expert rows
 //            come first; with in-kernel routing each block ranks the experts
-//            (hf_select.h) while the loads of its wavefronts' first (shared)
-//            rows are in flight, so routing adds no serial step.
+//            (hf_select.h) once its wavefronts' first (shared) rows have
+//            landed, while the other blocks' rows keep HBM busy.
 //   down:    one block per set of output rows (groups of U consecutive rows,
 //            interleaved across blocks so each batch of the chip reads one
 //            contiguous stretch of every slot's down matrix), one wavefront
@@ -129,8 +129,11 @@ __global__ __launch_bounds__(256) void gateup_t1_kernel(const float* __restrict_
     bool preloaded = false;
     if (ROUTE) {
         __shared__ SelectSmem sm;
-        // Scores first, then the first (shared) row's weights: the block ranks
-        // the experts while those weights stream in.
+        // Scores first, then the first (shared) row's weights (routing-free).
+        // The selection's block barriers wait for those weight loads as well;
+        // a version that let the ranking run ahead of them (x and scores by LDS
+        // DMA, LDS-only barriers) measured the same: the shared rows keep HBM
+        // saturated meanwhile.
         SelectRegs regs;
         select_fetch(scores, c.E, regs);
         if (q < total && q < shared_items) {
