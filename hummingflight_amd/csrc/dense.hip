@@ -9,7 +9,12 @@
 //           products in a fixed order), no routed slots;
 //   T > 1:  the grouped GEMM multiplies every token row by the one weight set
 //           (one group, no dispatch): gate/up with the SwiGLU epilogue into
-//           h (BF16 hi + lo), then down straight into out.
+//           h, then down straight into out.  With prefill tiles h is FP16 and
+//           the down projection multiplies that one half (against its
+//           weights converted to FP16), as the MoE layer's prefill does; a
+//           second gate/up pass writes the BF16 hi + lo halves instead when
+//           some h does not fit FP16 (a device flag; the pass otherwise exits
+//           at once).  Smaller batches keep the hi + lo halves.
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 
@@ -17,7 +22,7 @@ namespace hf {
 
 void dense_workspace_free() {
     DenseWorkspace& w = g.dws;
-    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl})
+    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl, (void*)w.h16})
         if (p) hipFree(p);
     w = DenseWorkspace{};
 }
@@ -30,6 +35,7 @@ static int dense_workspace_reserve(int inter) {
     hipError_t e = hipMalloc(&w.h1, sizeof(float) * (size_t)inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hh, 2 * (size_t)tokens * inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hl, 2 * (size_t)tokens * inter);
+    if (e == hipSuccess && tokens) e = hipMalloc(&w.h16, 2 * (size_t)tokens * inter);
     if (e != hipSuccess) {
         dense_workspace_free();
         return fail(HFMOE_ERR_OUT_OF_MEMORY, "dense MLP workspace (inter %d, %d tokens): %s", inter, tokens,
@@ -104,8 +110,18 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     gu.h_hi = w.hh;
     gu.h_lo = w.hl;
     gu.ksplit = 1;
+    // Prefill tiles (the split kernel) take h as FP16; flag cleared by split_bf16.
+    const bool f16 = TR != kGemmTileRows;
+    gu.h_f16 = f16 ? w.h16 : nullptr;
+    gu.h_f16_bad = gw.lo_flag + 1;
     prof_begin(p, "dense_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "dense gate/up gemm");
+    if (f16) {
+        GemmArgs hl = gu;
+        hl.h_f16 = nullptr;
+        hl.run_if = gu.h_f16_bad;
+        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, hl, gemm_blocks(TR), s), "dense gate/up hi/lo gemm");
+    }
     GemmArgs dn{};
     dn.K = I;
     dn.N = c.d;
@@ -116,6 +132,8 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     dn.rows_total = T;
     dn.a_hi = w.hh;
     dn.a_lo = w.hl;
+    dn.a_f16 = gu.h_f16;
+    dn.a_f16_bad = gu.h_f16_bad;
     dn.b_fixed0 = L.dev.sd;
     dn.b_ld = I;
     dn.out_f32 = out;

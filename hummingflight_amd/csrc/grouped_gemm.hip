@@ -929,7 +929,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
-    const bool use_f16 = EPI == EPI_SCATTER && a.a_f16 && *a.a_f16_bad == 0u;
+    // FP16 activations (an FP16 copy of h) for the down projections: the MoE
+    // layer's (SCATTER) and the dense layer's (PARTIAL, one K split).
+    constexpr bool F16_OK = EPI != EPI_SWIGLU;
+    const bool use_f16 = F16_OK && a.a_f16 && *a.a_f16_bad == 0u;
     // One item, then a barrier: every wavefront is done with the LDS rings
     // before the next item's loads land in them.  (The item's own loads have
     // all landed; its stores need not have.)
@@ -938,7 +941,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
             on_setup();
             return;
         }
-        if constexpr (EPI == EPI_SCATTER) {
+        if constexpr (F16_OK) {
             if (use_f16) {
                 gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave, on_setup);
                 lds_barrier();

@@ -80,6 +80,7 @@ struct DenseWorkspace {
     float* h1 = nullptr;     // [inter] T = 1 intermediate
     uint16_t* hh = nullptr;  // [max_tokens, inter] h hi (multi-token path)
     uint16_t* hl = nullptr;  // [max_tokens, inter] h lo
+    uint16_t* h16 = nullptr; // [max_tokens, inter] h as FP16 (prefill tiles)
     int inter = 0;
     int tokens = 0;
 };

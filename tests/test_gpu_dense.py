@@ -24,14 +24,14 @@ pytestmark = pytest.mark.gpu
 class Dense:
     """A seeded dense layer on the device and its host copy."""
 
-    def __init__(self, hidden, inter, seed, layer=0, with_norm=True):
+    def __init__(self, hidden, inter, seed, layer=0, with_norm=True, std=0.02):
         self.hidden, self.inter, self.layer = hidden, inter, layer
         n = hidden * inter
-        self.host = [O.fill_bf16(n, seed, 100 + i, 0.0, 0.02) for i in range(3)]
+        self.host = [O.fill_bf16(n, seed, 100 + i, 0.0, std) for i in range(3)]
         self.norm = O.fill_bf16(hidden, seed, 103, 1.0, 0.05) if with_norm else None
         self.dev = [capi.DeviceBuffer(2 * n) for _ in range(3)]
         for i, b in enumerate(self.dev):
-            synth.fill_bf16(b.ptr, n, seed, 100 + i, 0.0, 0.02)
+            synth.fill_bf16(b.ptr, n, seed, 100 + i, 0.0, std)
         self.norm_dev = None
         if with_norm:
             self.norm_dev = capi.DeviceBuffer(2 * hidden)
@@ -91,6 +91,42 @@ def test_dense_glm_shape(hf):
     for t in (0, 7):
         assert_close(y[t], L.ref(x[t]), f"token {t}")
     assert_close(L.forward(x[:1])[0], L.ref(x[0]), "decode")
+    L.free()
+
+
+def test_dense_glm_shape_prefill_tiles(hf):
+    # T >= 192: prefill tiles, h as FP16 into the down projection.
+    H, I, T = 6144, 12288, 256
+    configure(H, 2048, 256, T)
+    L = Dense(H, I, seed=35)
+    x = np.random.default_rng(35).standard_normal((T, H)).astype(np.float32)
+    y = L.forward(x)
+    for t in (0, 129, T - 1):
+        assert_close(y[t], L.ref(x[t]), f"token {t}")
+    L.free()
+
+
+def test_dense_h_overflowing_fp16_takes_hi_lo(hf):
+    # Weights ~N(0, 4): |h| passes FP16's 65504, so the gate/up epilogue flags
+    # it and the second pass writes the BF16 hi + lo halves the down
+    # projection then multiplies.  At that weight scale an output is a small
+    # residual of terms near 1e6, so FP32 summation order alone moves it by
+    # ~1e-5 of the token's largest output: the absolute floor is 1e-4 of that
+    # instead of 2e-3 (as for the MoE layer's prefill fallback test).
+    H, I, T = 1024, 3072, 300
+    configure(H, 512, 64, T)
+    L = Dense(H, I, seed=36, std=4.0)
+    x = np.random.default_rng(36).standard_normal((T, H)).astype(np.float32)
+    y = L.forward(x)
+    assert np.all(np.isfinite(y))
+    for t in (0, 150, T - 1):
+        ref = L.ref(x[t]).astype(np.float64)
+        err = np.abs(y[t] - ref)
+        assert np.all(err <= 1e-2 * np.abs(ref) + 1e-4 * np.abs(ref).max()), f"token {t}: {err.max()}"
+    g = O.bf16_to_f32(L.host[0]).reshape(I, H) @ x[0].astype(np.float64)
+    u = O.bf16_to_f32(L.host[1]).reshape(I, H) @ x[0].astype(np.float64)
+    h_max = np.max(np.abs(g / (1.0 + np.exp(-g)) * u))
+    assert h_max > 65504.0, h_max  # the case exercises the hi + lo pass
     L.free()
 
 
