@@ -22,7 +22,7 @@ namespace hf {
 
 void dense_workspace_free() {
     DenseWorkspace& w = g.dws;
-    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl, (void*)w.h16})
+    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl, (void*)w.h16, (void*)w.part})
         if (p) hipFree(p);
     w = DenseWorkspace{};
 }
@@ -36,6 +36,7 @@ static int dense_workspace_reserve(int inter) {
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hh, 2 * (size_t)tokens * inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hl, 2 * (size_t)tokens * inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.h16, 2 * (size_t)tokens * inter);
+    if (e == hipSuccess && tokens) e = hipMalloc(&w.part, sizeof(float) * 2 * (size_t)tokens * g.cfg.d);
     if (e != hipSuccess) {
         dense_workspace_free();
         return fail(HFMOE_ERR_OUT_OF_MEMORY, "dense MLP workspace (inter %d, %d tokens): %s", inter, tokens,
@@ -55,6 +56,26 @@ static int dense_slice(int inter) {
     for (int n = (inter + 4095) / 4096; n <= kMaxSlots; ++n)
         if (inter % n == 0 && (inter / n) % 8 == 0) return inter / n;
     return 0;
+}
+
+// K splits of the down projection with prefill tiles, whose workgroups take
+// their items statically: the fewest splits that minimise the rounds of items
+// per workgroup, counted in whole-K item times (384 items on 256 workgroups:
+// two rounds of whole items, against three of half items with two splits),
+// each split a whole number of 64-wide K stages and the partials
+// ([splits, T, hidden] FP32) within the workspace's 2 * max_tokens rows.
+static int dense_down_ksplit(int items, int stages, int T, int blocks) {
+    int best = 1;
+    double best_rounds = (double)((items + blocks - 1) / blocks);
+    for (int k = 2; k <= 8; ++k) {
+        if (stages % k || (size_t)k * T > 2 * (size_t)g.dws.tokens) continue;
+        const double rounds = (double)(((size_t)items * k + blocks - 1) / blocks) / k;
+        if (rounds < best_rounds - 1e-9) {
+            best = k;
+            best_rounds = rounds;
+        }
+    }
+    return best;
 }
 
 #define HF_CHECK_LAUNCH(expr, what)                      \
@@ -137,9 +158,14 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     dn.b_fixed0 = L.dev.sd;
     dn.b_ld = I;
     dn.out_f32 = out;
-    dn.ksplit = 1;
+    dn.ksplit = f16 ? dense_down_ksplit(dn.m_tiles * dn.n_tiles, I / kGemmTileK, T, gemm_blocks(TR)) : 1;
+    if (dn.ksplit > 1) dn.out_f32 = w.part;
     prof_begin(p, "dense_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, dn, gemm_blocks(TR), s), "dense down gemm");
+    if (dn.ksplit > 1) {
+        prof_begin(p, "dense_down_sum", s);
+        HF_CHECK_LAUNCH(launch_sum_splits(w.part, dn.ksplit, (size_t)T * c.d, out, s), "dense down split sum");
+    }
     return HFMOE_OK;
 }
 

@@ -1032,6 +1032,28 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
     if (__ballot(nz) != 0ull && (threadIdx.x & 63) == 0) atomicOr(flag, 1u);
 }
 
+// out[i] = ((part[0][i] + part[1][i]) + part[2][i]) + ...: the K splits of a
+// PARTIAL GEMM ([ks][n] FP32) summed in split order, four values per thread
+// (n a multiple of 4, both arrays 16-byte aligned).
+__global__ void sum_splits_kernel(const float* __restrict__ part, int ks, size_t n4, float* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(part) + i);
+        for (int k = 1; k < ks; ++k) v += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(part) + k * n4 + i);
+        reinterpret_cast<f32x4_t*>(out)[i] = v;
+    }
+}
+
+hipError_t launch_sum_splits(const float* part, int ks, size_t n, float* out, hipStream_t s) {
+    if (ks < 1 || n % 4 || ((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out)) & 15))
+        return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    size_t blocks = (n4 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    return launch(sum_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, ks, n4, out);
+}
+
 __global__ void clear_u32_kernel(unsigned* p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0u;

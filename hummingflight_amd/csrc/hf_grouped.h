@@ -78,6 +78,8 @@ struct GemmArgs {
 hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream_t s);
 // p[0, n) = 0 by a kernel (graph-capture safe, unlike a memset node).
 hipError_t launch_clear_u32(unsigned* p, int n, hipStream_t s);
+// out[i] = sum over k < ks of part[k * n + i], in k order (n a multiple of 4).
+hipError_t launch_sum_splits(const float* part, int ks, size_t n, float* out, hipStream_t s);
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s);
 // out[t] = sum_r wts[t, r] * y[t*k + r] (+ y[shared_row0 + t] when shared_row0 >= 0); d % 4 == 0.

@@ -106,6 +106,19 @@ def test_dense_glm_shape_prefill_tiles(hf):
     L.free()
 
 
+@pytest.mark.parametrize("H,I,T", [(1024, 3072, 200), (6144, 12288, 256)])
+def test_dense_down_k_splits(hf, H, I, T):
+    # max_tokens well above T: the down projection's few items (one M tile)
+    # are split 8 ways along K into partials summed in split order.
+    configure(H, 2048 if H == 6144 else 512, 256 if H == 6144 else 64, 2048)
+    L = Dense(H, I, seed=37)
+    x = np.random.default_rng(37).standard_normal((T, H)).astype(np.float32)
+    y = L.forward(x)
+    for t in (0, T // 2, T - 1):
+        assert_close(y[t], L.ref(x[t]), f"T={T} token {t}")
+    L.free()
+
+
 def test_dense_h_overflowing_fp16_takes_hi_lo(hf):
     # Weights ~N(0, 4): |h| passes FP16's 65504, so the gate/up epilogue flags
     # it and the second pass writes the BF16 hi + lo halves the down
