@@ -110,8 +110,8 @@ int orc_topk_flat(const float* scores, int E, const float* bias, int k,
     return k;
 }
 
-/* Group-limited selection (DeepSeek-V3 noaux_tc convention; north-star
- * extension, see oracle.h). */
+/* Group-limited selection (DeepSeek-V3 noaux_tc convention; beyond the
+ * reference, see oracle.h). */
 int orc_topk_grouped(const float* scores, int E, const float* bias, int k,
                      int n_group, int topk_group, float scale, int norm,
                      int* idx, float* w) {

@@ -13,7 +13,7 @@
  * reference), glibc expf for std::exp(float).
  *
  * Functions that go beyond the reference (group-limited selection, dispatch,
- * the seeded generator) are north-star extensions; each says how it is pinned.
+ * the seeded generator) say so and how each is pinned.
  */
 #ifndef HF_ORACLE_H
 #define HF_ORACLE_H
@@ -54,7 +54,7 @@ void orc_sigmoid_n(const float* x, float* y, int64_t n);
 int orc_topk_flat(const float* scores, int E, const float* bias, int k,
                   float scale, int norm, int* idx, float* w);
 
-/* ---- group-limited noaux_tc top-k (north-star extension; the reference parses
+/* ---- group-limited noaux_tc top-k (beyond the reference, which parses
  * topk_group but never uses it, src/model/config.cpp:117) ----
  * E experts in n_group equal contiguous groups.  Group score = sum of the two
  * largest biased scores in the group (largest + second largest, one float add;
@@ -68,7 +68,7 @@ int orc_topk_grouped(const float* scores, int E, const float* bias, int k,
                      int* idx, float* w);
 
 /* ---- dispatch: stable counting sort of (token, rank) pairs by expert
- * (north-star extension; the reference loops token by token,
+ * (beyond the reference, which loops token by token,
  * glm_forward.cpp:755, and expert by expert, :581) ----
  * idx: int [T*k] expert per pair, pair p = t*k + r.
  * counts[E], offsets[E+1] (exclusive scan), perm[T*k]: pair ids ordered by
@@ -146,7 +146,7 @@ int orc_moe_combine(const orc_moe_cfg* cfg, const orc_moe_weights* W,
 double orc_moe_layer_bench(const orc_moe_cfg* cfg, const orc_moe_weights* W, const float* x, float* out,
                            int avx2, void* copy_scratch, int iters);
 
-/* ---- seeded counter-based generator (north-star extension) ----
+/* ---- seeded counter-based generator (beyond the reference) ----
  * Element i of tensor `tensor` under `seed`: three SplitMix64 outputs give
  * twelve 16-bit uniforms; z = (sum - 393210) / 65536 (exact, mean 0, var ~1,
  * Irwin-Hall(12) approximation of N(0,1)); value = z*std (rounded) + mean
