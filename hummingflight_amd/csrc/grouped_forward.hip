@@ -184,12 +184,19 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
-    // Prefill tiles: h as FP16, which the down projection multiplies as one
-    // half (against FP16-converted weights).  Should any value not fit FP16,
-    // a second pass (which otherwise exits at once) writes the BF16 hi / lo
-    // halves for the down projection to take instead.
-    gu.h_f16 = TR == kPrefillTileRows ? w.h16 : nullptr;
+    // Prefill tiles: the routed experts' h as FP16, which the down projection
+    // multiplies as one half (against FP16-converted weights); the shared
+    // expert's rows keep the BF16 hi / lo halves (its output enters with
+    // weight 1: FP16 there would take the worst output of a full-shape prefill
+    // to ~0.95 of the 2e-3 + 1e-2 tolerance, ~0.6 without it).  Should any
+    // FP16 value not fit, a second pass (which otherwise exits at once) writes
+    // the hi / lo halves of every row for the down projection to take instead.
+    // HFMOE_PREFILL_EXACT_H=1 keeps every row's h exact (the down projection's
+    // MFMA work and activation bytes doubled for the routed rows).
+    const bool f16_h = TR == kPrefillTileRows && env_int("HFMOE_PREFILL_EXACT_H", 0) == 0;
+    gu.h_f16 = f16_h ? w.h16 : nullptr;
     gu.h_f16_bad = w.lo_flag + 1;
+    gu.f16_rows = P;  // the routed pairs; the shared expert's rows keep hi + lo
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
     if (gu.h_f16) {
@@ -224,6 +231,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
     dn.a_f16 = gu.h_f16;
     dn.a_f16_bad = w.lo_flag + 1;
+    dn.f16_rows = P;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;

@@ -205,8 +205,8 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
 // column col0 + 16*cb + q (q = 0..3).  SWIGLU: blocks [0, NCB/2) are gate and
 // [NCB/2, NCB) the matching up columns; writes h = silu(g) * u
 // (glm_forward.cpp:444-446), 8 bytes per array: as FP16 alone when a.h_f16 is
-// given (setting *a.h_f16_bad when a value does not fit FP16), else as BF16
-// hi/lo.  PARTIAL / SCATTER: 16-byte FP32 stores (row stride N is a multiple
+// given and gr < a.f16_rows (setting *a.h_f16_bad when a value does not fit
+// FP16), else as BF16 hi/lo.  PARTIAL / SCATTER: 16-byte FP32 stores (row stride N is a multiple
 // of 4 whenever N is a multiple of 64; a ragged router width falls back to
 // single floats) to output row orow_idx (SCATTER: the token-order row of gr;
 // PARTIAL: gr).  NT: non-temporal stores.
@@ -225,7 +225,7 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                 hv[cb][q] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[cb + NCB / 2][q];
             }
         bool bad = false;
-        if (a.h_f16) {  // FP16 h, one 8-byte store per column block
+        if (a.h_f16 && gr < a.f16_rows) {  // FP16 h, one 8-byte store per column block
             uint16_t* frow = a.h_f16 + (size_t)gr * a.N;
 #pragma unroll
             for (int cb = 0; cb < NCB / 2; ++cb) {
@@ -267,7 +267,7 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                 *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
             }
         }
-        if (bad) atomicOr(a.h_f16_bad, 1u);
+        if (bad) *a.h_f16_bad = 1u;  // 0 -> 1 only, read by later kernels: a plain store
     } else {
         float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + orow_idx) * a.N
                                          : a.out_f32 + (size_t)orow_idx * a.N;
@@ -929,9 +929,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
-    // FP16 activations (an FP16 copy of h) for the down projections: the MoE
-    // layer's (SCATTER) and the dense layer's (PARTIAL, one K split).
-    constexpr bool F16_OK = EPI != EPI_SWIGLU;
+    // FP16 activations (an FP16 copy of h) for the MoE down projection.
+    constexpr bool F16_OK = EPI == EPI_SCATTER;
     const bool use_f16 = F16_OK && a.a_f16 && *a.a_f16_bad == 0u;
     // One item, then a barrier: every wavefront is done with the LDS rings
     // before the next item's loads land in them.  (The item's own loads have
@@ -942,7 +941,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
             return;
         }
         if constexpr (F16_OK) {
-            if (use_f16) {
+            const int mt = item / a.ksplit / a.n_tiles;
+            if (use_f16 && (a.tile_row0 ? a.tile_row0[mt] : mt * ROWS) < a.f16_rows) {
                 gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave, on_setup);
                 lds_barrier();
                 return;
@@ -992,7 +992,7 @@ __global__ void combine_kernel(const float* __restrict__ wts, const float* __res
     reinterpret_cast<float4*>(out)[i4] = m;
 }
 
-// x FP32 [n] -> BF16 hi/lo; *flag |= 1 when any lo is nonzero.  Eight values
+// x FP32 [n] -> BF16 hi/lo; *flag = 1 when any lo is nonzero.  Eight values
 // per thread and step (two 16-byte loads, one 16-byte store per half) when x
 // is 16-byte aligned, then single values for the rest.  x is read once:
 // non-temporal loads; hi/lo are read again by the GEMMs that follow.
@@ -1029,7 +1029,11 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
         lo[i] = l;
         nz |= (l & 0x7FFF) != 0;
     }
-    if (__ballot(nz) != 0ull && (threadIdx.x & 63) == 0) atomicOr(flag, 1u);
+    // A plain store: the flag only goes from 0 (cleared by an earlier kernel)
+    // to 1 and is read by later kernels; with FP32 activations every
+    // wavefront sets it, and as many device-scope atomics on one address
+    // serialise at the memory (x split of 4096 x 6144: 199 -> 37 us).
+    if (__ballot(nz) != 0ull && (threadIdx.x & 63) == 0) *flag = 1u;
 }
 
 // out[i] = ((part[0][i] + part[1][i]) + part[2][i]) + ...: the K splits of a

@@ -80,7 +80,6 @@ struct DenseWorkspace {
     float* h1 = nullptr;     // [inter] T = 1 intermediate
     uint16_t* hh = nullptr;  // [max_tokens, inter] h hi (multi-token path)
     uint16_t* hl = nullptr;  // [max_tokens, inter] h lo
-    uint16_t* h16 = nullptr; // [max_tokens, inter] h as FP16 (prefill tiles)
     float* part = nullptr;   // [2 * max_tokens, hidden] K-split partials of the down projection
     int inter = 0;
     int tokens = 0;

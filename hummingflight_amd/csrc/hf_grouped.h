@@ -68,6 +68,11 @@ struct GemmArgs {
     // consumer needs the hi / lo halves: see run_if).
     uint16_t* h_f16;
     unsigned* h_f16_bad;
+    // Rows [0, f16_rows) take the FP16 h (SWIGLU: written as FP16; down: the
+    // FP16 operand); later rows keep the BF16 hi / lo halves.  The MoE layer
+    // sets it to T * k, so the shared expert (weight 1 in the output, the
+    // largest share of FP16 rounding error) stays exact.  0: none.
+    int f16_rows;
     // When not null, the launch does nothing unless *run_if != 0 (a second
     // gate/up pass that writes the BF16 hi / lo halves only after some h did
     // not fit FP16).

@@ -94,8 +94,22 @@ def test_dense_glm_shape(hf):
     L.free()
 
 
+def ref_all(L, x):
+    """The dense MLP of every token in float32 (the oracle's weights; FP32
+    summation-order differences are ~1e-6 of the outputs, far inside the
+    tolerance), for checks over every output of a batch."""
+    H, I = L.hidden, L.inter
+    Wg, Wu, Wd = (O.bf16_to_f32(m) for m in L.host)
+    g = x @ Wg.reshape(I, H).T
+    u = x @ Wu.reshape(I, H).T
+    h = g / (1.0 + np.exp(-g)) * u
+    return h @ Wd.reshape(H, I).T
+
+
 def test_dense_glm_shape_prefill_tiles(hf):
-    # T >= 192: prefill tiles, h as FP16 into the down projection.
+    # T >= 192: prefill tiles (h as BF16 hi + lo, two K splits of the down
+    # projection); every output against the float32 reference, three tokens
+    # against the oracle.
     H, I, T = 6144, 12288, 256
     configure(H, 2048, 256, T)
     L = Dense(H, I, seed=35)
@@ -103,6 +117,7 @@ def test_dense_glm_shape_prefill_tiles(hf):
     y = L.forward(x)
     for t in (0, 129, T - 1):
         assert_close(y[t], L.ref(x[t]), f"token {t}")
+    assert_close(y, ref_all(L, x), "every output")
     L.free()
 
 
@@ -116,16 +131,16 @@ def test_dense_down_k_splits(hf, H, I, T):
     y = L.forward(x)
     for t in (0, T // 2, T - 1):
         assert_close(y[t], L.ref(x[t]), f"T={T} token {t}")
+    assert_close(y, ref_all(L, x), f"T={T} every output")
     L.free()
 
 
-def test_dense_h_overflowing_fp16_takes_hi_lo(hf):
-    # Weights ~N(0, 4): |h| passes FP16's 65504, so the gate/up epilogue flags
-    # it and the second pass writes the BF16 hi + lo halves the down
-    # projection then multiplies.  At that weight scale an output is a small
-    # residual of terms near 1e6, so FP32 summation order alone moves it by
-    # ~1e-5 of the token's largest output: the absolute floor is 1e-4 of that
-    # instead of 2e-3 (as for the MoE layer's prefill fallback test).
+def test_dense_large_weights(hf):
+    # Weights ~N(0, 4): |h| passes 65504 (beyond FP16) on prefill tiles.  At
+    # that weight scale an output is a small residual of terms near 1e6, so
+    # FP32 summation order alone moves it by ~1e-5 of the token's largest
+    # output: the absolute floor is 1e-4 of that instead of 2e-3 (as for the
+    # MoE layer's prefill fallback test).
     H, I, T = 1024, 3072, 300
     configure(H, 512, 64, T)
     L = Dense(H, I, seed=36, std=4.0)
@@ -139,7 +154,7 @@ def test_dense_h_overflowing_fp16_takes_hi_lo(hf):
     g = O.bf16_to_f32(L.host[0]).reshape(I, H) @ x[0].astype(np.float64)
     u = O.bf16_to_f32(L.host[1]).reshape(I, H) @ x[0].astype(np.float64)
     h_max = np.max(np.abs(g / (1.0 + np.exp(-g)) * u))
-    assert h_max > 65504.0, h_max  # the case exercises the hi + lo pass
+    assert h_max > 65504.0, h_max
     L.free()
 
 
