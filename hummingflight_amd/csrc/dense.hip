@@ -129,6 +129,11 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     gu.h_hi = w.hh;
     gu.h_lo = w.hl;
     gu.ksplit = 1;
+    // Every M tile multiplies the same weights: XCDs split the N tiles and
+    // walk M fastest, so a weight tile is read once per XCD and round rather
+    // than once per M tile (items are independent: results are unchanged).
+    const int by_ntile = TR == kDenseTileRows ? env_int("HFMOE_DENSE_BY_NTILE", 1) : 0;
+    gu.by_ntile = by_ntile;
     prof_begin(p, "dense_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "dense gate/up gemm");
     GemmArgs dn{};
@@ -147,6 +152,7 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     // Prefill tiles (the split kernel, items dealt statically): K splits.
     dn.ksplit = TR != kGemmTileRows ? dense_down_ksplit(dn.m_tiles * dn.n_tiles, I / kGemmTileK, T, gemm_blocks(TR)) : 1;
     if (dn.ksplit > 1) dn.out_f32 = w.part;
+    dn.by_ntile = by_ntile;
     prof_begin(p, "dense_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, dn, gemm_blocks(TR), s), "dense down gemm");
     if (dn.ksplit > 1) {

@@ -174,7 +174,15 @@ struct ItemRange {
     int begin, end, stride;  // local item indices begin, begin + stride, ... < end
     int xcd, nxcd, per_m;    // per_m = n_tiles * ksplit items per M tile
     bool by_mtile;
+    int by_ntile;            // nonzero: N tiles [xcd * n_local, +n_local), M tiles fastest
+    int n_local, m_tiles, ksplit;
     __device__ __forceinline__ int item(int li) const {
+        if (by_ntile) {
+            const int per_n = m_tiles * ksplit;
+            const int nt = xcd * n_local + li / per_n;
+            const int rem = li % per_n;
+            return ((rem / ksplit) * (per_m / ksplit) + nt) * ksplit + rem % ksplit;
+        }
         return by_mtile ? (xcd + nxcd * (li / per_m)) * per_m + li % per_m : li;
     }
 };
@@ -186,9 +194,16 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
     r.xcd = blockIdx.x % r.nxcd;
     r.stride = (int)gridDim.x / r.nxcd + (r.xcd < (int)gridDim.x % r.nxcd ? 1 : 0);
     r.per_m = a.n_tiles * a.ksplit;
-    r.by_mtile = DEAL_M && m_tiles >= r.nxcd;
+    r.m_tiles = m_tiles;
+    r.ksplit = a.ksplit;
+    r.by_ntile = a.by_ntile && !a.tile_group && r.nxcd > 1 && a.n_tiles % r.nxcd == 0;
+    r.n_local = a.n_tiles / r.nxcd;
+    r.by_mtile = !r.by_ntile && DEAL_M && m_tiles >= r.nxcd;
     const int local = blockIdx.x / r.nxcd;
-    if (r.by_mtile) {
+    if (r.by_ntile) {
+        r.begin = local;
+        r.end = r.n_local * m_tiles * a.ksplit;
+    } else if (r.by_mtile) {
         const int m_local = (m_tiles - r.xcd + r.nxcd - 1) / r.nxcd;
         r.begin = local;
         r.end = m_local * r.per_m;

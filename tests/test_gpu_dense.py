@@ -135,6 +135,24 @@ def test_dense_down_k_splits(hf, H, I, T):
     L.free()
 
 
+def test_dense_item_orders_bit_identical(hf, monkeypatch):
+    # Prefill tiles deal the items by N tile (each XCD a range of N tiles, M
+    # tiles fastest) unless HFMOE_DENSE_BY_NTILE=0 (each XCD whole M tiles):
+    # every item is computed the same way whichever workgroup takes it, so
+    # the two orders agree bit for bit; three M tiles, ragged last tile.
+    H, I, T = 6144, 12288, 600
+    configure(H, 2048, 256, T)
+    L = Dense(H, I, seed=39)
+    x = np.random.default_rng(39).standard_normal((T, H)).astype(np.float32)
+    y = L.forward(x)
+    monkeypatch.setenv("HFMOE_DENSE_BY_NTILE", "0")
+    y0 = L.forward(x)
+    monkeypatch.delenv("HFMOE_DENSE_BY_NTILE")
+    assert np.array_equal(y.view(np.uint32), y0.view(np.uint32))
+    assert_close(y, ref_all(L, x), "every output")
+    L.free()
+
+
 def test_dense_large_weights(hf):
     # Weights ~N(0, 4): |h| passes 65504 (beyond FP16) on prefill tiles.  At
     # that weight scale an output is a small residual of terms near 1e6, so
