@@ -174,14 +174,16 @@ struct ItemRange {
     int begin, end, stride;  // local item indices begin, begin + stride, ... < end
     int xcd, nxcd, per_m;    // per_m = n_tiles * ksplit items per M tile
     bool by_mtile;
-    int by_ntile;            // nonzero: N tiles [xcd * n_local, +n_local), M tiles fastest
-    int n_local, m_tiles, ksplit;
+    // by_ntile: this XCD's block of N tiles [n0, n0 + n_local) x M tiles
+    // [m0, m0 + m_cnt), M tiles fastest
+    bool by_ntile;
+    int n0, n_local, m0, m_cnt, ksplit;
     __device__ __forceinline__ int item(int li) const {
         if (by_ntile) {
-            const int per_n = m_tiles * ksplit;
-            const int nt = xcd * n_local + li / per_n;
+            const int per_n = m_cnt * ksplit;
+            const int nt = n0 + li / per_n;
             const int rem = li % per_n;
-            return ((rem / ksplit) * (per_m / ksplit) + nt) * ksplit + rem % ksplit;
+            return ((m0 + rem / ksplit) * (per_m / ksplit) + nt) * ksplit + rem % ksplit;
         }
         return by_mtile ? (xcd + nxcd * (li / per_m)) * per_m + li % per_m : li;
     }
@@ -194,15 +196,24 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
     r.xcd = blockIdx.x % r.nxcd;
     r.stride = (int)gridDim.x / r.nxcd + (r.xcd < (int)gridDim.x % r.nxcd ? 1 : 0);
     r.per_m = a.n_tiles * a.ksplit;
-    r.m_tiles = m_tiles;
     r.ksplit = a.ksplit;
-    r.by_ntile = a.by_ntile && !a.tile_group && r.nxcd > 1 && a.n_tiles % r.nxcd == 0;
-    r.n_local = a.n_tiles / r.nxcd;
+    // a.by_ntile N groups x (nxcd / a.by_ntile) M groups, one block per XCD;
+    // every group the same size, else whole N-tile ranges (one M group)
+    int gn = a.by_ntile;
+    if (gn > 0 && (r.nxcd % gn || a.n_tiles % gn || m_tiles % (r.nxcd / gn))) gn = r.nxcd;
+    r.by_ntile = gn > 0 && !a.tile_group && r.nxcd > 1 && a.n_tiles % gn == 0;
+    if (r.by_ntile) {
+        const int gm = r.nxcd / gn;
+        r.n_local = a.n_tiles / gn;
+        r.n0 = (r.xcd % gn) * r.n_local;
+        r.m_cnt = m_tiles / gm;
+        r.m0 = (r.xcd / gn) * r.m_cnt;
+    }
     r.by_mtile = !r.by_ntile && DEAL_M && m_tiles >= r.nxcd;
     const int local = blockIdx.x / r.nxcd;
     if (r.by_ntile) {
         r.begin = local;
-        r.end = r.n_local * m_tiles * a.ksplit;
+        r.end = r.n_local * r.m_cnt * a.ksplit;
     } else if (r.by_mtile) {
         const int m_local = (m_tiles - r.xcd + r.nxcd - 1) / r.nxcd;
         r.begin = local;

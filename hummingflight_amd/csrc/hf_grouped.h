@@ -73,11 +73,12 @@ struct GemmArgs {
     // sets it to T * k, so the shared expert (weight 1 in the output, the
     // largest share of FP16 rounding error) stays exact.  0: none.
     int f16_rows;
-    // Nonzero (one group, statically dealt items; taken when n_tiles is a
-    // multiple of the XCD count): each XCD takes a contiguous range of N tiles
-    // and walks its items with M tiles fastest, so the workgroups of an XCD
-    // that share a weight tile stream it together through that XCD's L2, and
-    // the activations (every M tile) are what is read again from the fabric.
+    // Nonzero (one group, statically dealt items): the XCDs split the tiles
+    // into by_ntile N groups x (XCDs / by_ntile) M groups, one block each,
+    // and walk their block's items with M tiles fastest, so the workgroups of
+    // an XCD that share a weight tile stream it together through that XCD's
+    // L2.  Groups must divide evenly; else (XCDs) N groups and one M group,
+    // when the N tiles divide; else the usual dealing.
     int by_ntile;
     // When not null, the launch does nothing unless *run_if != 0 (a second
     // gate/up pass that writes the BF16 hi / lo halves only after some h did

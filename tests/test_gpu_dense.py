@@ -135,12 +135,15 @@ def test_dense_down_k_splits(hf, H, I, T):
     L.free()
 
 
-def test_dense_item_orders_bit_identical(hf, monkeypatch):
-    # Prefill tiles deal the items by N tile (each XCD a range of N tiles, M
+@pytest.mark.parametrize("T", [512, 600])
+def test_dense_item_orders_bit_identical(hf, monkeypatch, T):
+    # Prefill tiles deal the items in blocks of N tiles x M tiles per XCD (M
     # tiles fastest) unless HFMOE_DENSE_BY_NTILE=0 (each XCD whole M tiles):
     # every item is computed the same way whichever workgroup takes it, so
-    # the two orders agree bit for bit; three M tiles, ragged last tile.
-    H, I, T = 6144, 12288, 600
+    # the two orders agree bit for bit.  T = 512: two M tiles, 4 N groups x 2
+    # M groups; T = 600: three M tiles (the last ragged), which do not split
+    # in two, so 8 N groups x 1.
+    H, I = 6144, 12288
     configure(H, 2048, 256, T)
     L = Dense(H, I, seed=39)
     x = np.random.default_rng(39).standard_normal((T, H)).astype(np.float32)
