@@ -34,7 +34,10 @@ static int dense_workspace_reserve(int inter) {
     hipError_t e = hipMalloc(&w.h1, sizeof(float) * (size_t)inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hh, 2 * (size_t)tokens * inter);
     if (e == hipSuccess && tokens) e = hipMalloc(&w.hl, 2 * (size_t)tokens * inter);
-    if (e == hipSuccess && tokens) e = hipMalloc(&w.part, sizeof(float) * 2 * (size_t)tokens * g.cfg.d);
+    // Partials for up to 8 K splits of a short prompt (one M tile leaves the
+    // down projection 24 items), 2 of a long one.
+    const int part_rows = std::max(2 * tokens, std::min(8 * tokens, 4096));
+    if (e == hipSuccess && tokens) e = hipMalloc(&w.part, sizeof(float) * (size_t)part_rows * g.cfg.d);
     if (e != hipSuccess) {
         dense_workspace_free();
         return fail(HFMOE_ERR_OUT_OF_MEMORY, "dense MLP workspace (inter %d, %d tokens): %s", inter, tokens,
@@ -42,6 +45,7 @@ static int dense_workspace_reserve(int inter) {
     }
     w.inter = inter;
     w.tokens = tokens;
+    w.part_rows = tokens ? part_rows : 0;
     return HFMOE_OK;
 }
 
@@ -61,12 +65,12 @@ static int dense_slice(int inter) {
 // per workgroup, counted in whole-K item times (384 items on 256 workgroups:
 // two rounds of whole items, against three of half items with two splits),
 // each split a whole number of 64-wide K stages and the partials
-// ([splits, T, hidden] FP32) within the workspace's 2 * max_tokens rows.
+// ([splits, T, hidden] FP32) within the workspace's part_rows.
 static int dense_down_ksplit(int items, int stages, int T, int blocks) {
     int best = 1;
     double best_rounds = (double)((items + blocks - 1) / blocks);
     for (int k = 2; k <= 8; ++k) {
-        if (stages % k || (size_t)k * T > 2 * (size_t)g.dws.tokens) continue;
+        if (stages % k || (size_t)k * T > (size_t)g.dws.part_rows) continue;
         const double rounds = (double)(((size_t)items * k + blocks - 1) / blocks) / k;
         if (rounds < best_rounds - 1e-9) {
             best = k;
@@ -108,6 +112,8 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
         return HFMOE_OK;
     }
     GroupedWorkspace& gw = g.gws;
+    // From 192 tokens on, the prefill tiles (measured faster than 128-row
+    // tiles at every T from 256 to 1024).
     const int TR = T >= 192 ? kDenseTileRows : kGemmTileRows;
     const int I = L.dense_inter;
     prof_begin(p, "split_x", s);

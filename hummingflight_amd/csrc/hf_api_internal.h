@@ -80,9 +80,10 @@ struct DenseWorkspace {
     float* h1 = nullptr;     // [inter] T = 1 intermediate
     uint16_t* hh = nullptr;  // [max_tokens, inter] h hi (multi-token path)
     uint16_t* hl = nullptr;  // [max_tokens, inter] h lo
-    float* part = nullptr;   // [2 * max_tokens, hidden] K-split partials of the down projection
+    float* part = nullptr;   // [part_rows, hidden] K-split partials of the down projection
     int inter = 0;
     int tokens = 0;
+    int part_rows = 0;       // max(2 * max_tokens, min(8 * max_tokens, 4096))
 };
 
 struct Pending {
