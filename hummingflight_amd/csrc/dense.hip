@@ -60,8 +60,8 @@ static int dense_slice(int inter) {
     return 0;
 }
 
-// K splits of the down projection with prefill tiles, whose workgroups take
-// their items statically: the fewest splits that minimise the rounds of items
+// K splits of the down projection (both tile kinds take their items
+// statically here): the fewest splits that minimise the rounds of items
 // per workgroup, counted in whole-K item times (384 items on 256 workgroups:
 // two rounds of whole items, against three of half items with two splits),
 // each split a whole number of 64-wide K stages and the partials
@@ -158,8 +158,9 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     dn.b_fixed0 = L.dev.sd;
     dn.b_ld = I;
     dn.out_f32 = out;
-    // Prefill tiles (the split kernel, items dealt statically): K splits.
-    dn.ksplit = TR != kGemmTileRows ? dense_down_ksplit(dn.m_tiles * dn.n_tiles, I / kGemmTileK, T, gemm_blocks(TR)) : 1;
+    // K splits for both tile kinds: one M tile gives the down projection only
+    // hidden / 128 (128-row tiles) or hidden / 256 items.
+    dn.ksplit = dense_down_ksplit(dn.m_tiles * dn.n_tiles, I / kGemmTileK, T, gemm_blocks(TR));
     if (dn.ksplit > 1) dn.out_f32 = w.part;
     dn.by_ntile = by_ntile;
     prof_begin(p, "dense_down_gemm", s);

@@ -135,6 +135,22 @@ def test_dense_down_k_splits(hf, H, I, T):
     L.free()
 
 
+@pytest.mark.parametrize("T", [64, 191])
+def test_dense_glm_shape_small_batch_k_splits(hf, T):
+    # T < 192: 128-row tiles, the down projection's 48 items (96 at T = 191)
+    # split along K into partials summed in split order; every output against
+    # the float32 reference, two tokens against the oracle.
+    H, I = 6144, 12288
+    configure(H, 2048, 256, T)
+    L = Dense(H, I, seed=41)
+    x = np.random.default_rng(41).standard_normal((T, H)).astype(np.float32)
+    y = L.forward(x)
+    for t in (0, T - 1):
+        assert_close(y[t], L.ref(x[t]), f"T={T} token {t}")
+    assert_close(y, ref_all(L, x), f"T={T} every output")
+    L.free()
+
+
 @pytest.mark.parametrize("T", [512, 600])
 def test_dense_item_orders_bit_identical(hf, monkeypatch, T):
     # Prefill tiles deal the items in blocks of N tiles x M tiles per XCD (M
