@@ -140,7 +140,9 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     // per XCD and round rather than once per M tile, and an activation tile
     // once per round of the XCD's N tiles (measured at T = 4096 against 8 x 1
     // and 2 x 4 blocks).  Items are independent: results are unchanged.
-    // HFMOE_DENSE_BY_NTILE=0 deals whole M tiles per XCD instead.
+    // HFMOE_DENSE_BY_NTILE=0 deals whole M tiles per XCD instead.  (128-row
+    // tiles, at most two M tiles, measured the same either way: 8 x 1 blocks
+    // at T = 150 and 191 took gate/up 169-172 us like contiguous ranges.)
     const int by_ntile = TR == kDenseTileRows && env_int("HFMOE_DENSE_BY_NTILE", 1) != 0 ? 4 : 0;
     gu.by_ntile = by_ntile;
     prof_begin(p, "dense_gateup_gemm", s);
