@@ -67,8 +67,8 @@ class StreamOptions(C.Structure):
 class StreamCounters(C.Structure):
     _fields_ = [("lookups", C.c_uint64), ("hits", C.c_uint64), ("misses", C.c_uint64),
                 ("pred_staged", C.c_uint64), ("pred_consumed", C.c_uint64), ("pred_wasted", C.c_uint64),
-                ("pred_resident", C.c_uint64), ("copies", C.c_uint64), ("pinned", C.c_uint64),
-                ("slots", C.c_int32), ("reserved", C.c_int32)]
+                ("pred_resident", C.c_uint64), ("copies", C.c_uint64),
+                ("slots", C.c_int32), ("pinned", C.c_int32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_ if name != "reserved"}

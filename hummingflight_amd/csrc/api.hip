@@ -193,8 +193,11 @@ int hfmoe_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(HFMOE_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
-    int rc = noalloc_setup(device);
-    if (rc) return rc;
+    // The allocation-free entry point's scratch address is optional: when it
+    // cannot be taken the library still initialises, and only
+    // hfmoe_moe_forward_noalloc reports HFMOE_ERR_NOT_INITIALIZED (with this
+    // reason).
+    noalloc_setup(device);
     g.device = device;
     g.num_cus = prop.multiProcessorCount;
     g.total_mem = prop.totalGlobalMem;

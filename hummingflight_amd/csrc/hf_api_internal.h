@@ -189,7 +189,7 @@ int forward_t1(LayerState& L, const float* x, float* out, hipStream_t s, const h
 int forward_t1_on(LayerState& L, const float* x, float* out, hipStream_t s, const T1Buffers& b, bool profile);
 // noalloc.hip: the device address of this device's static scratch array
 // (hipGetSymbolAddress, once per device; called by hfmoe_init).
-int noalloc_setup(int device);
+void noalloc_setup(int device);  // never fails init: see noalloc.hip
 int forward_tokenwise(LayerState& L, const float* x, int T, float* out, hipStream_t s,
                       const hfmoe_route_debug* dbg);
 int copy_debug(const hfmoe_route_debug* dbg, int T, hipStream_t s);

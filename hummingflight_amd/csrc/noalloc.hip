@@ -10,7 +10,8 @@
 // stand-in, not a device pointer.  hfmoe_init calls noalloc_setup(device) with
 // that device current, which takes the device's own address of its copy with
 // hipGetSymbolAddress once, and the entry point passes only that address to
-// the kernels.
+// the kernels.  A failed setup does not fail hfmoe_init: only this entry
+// point is then unavailable.
 //
 // Every call on one GPU shares that GPU's array and the last call's contents
 // stay in it; each buffer is written in full by an earlier kernel of the same
@@ -30,6 +31,7 @@ constexpr int kMaxDevices = 64;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 unsigned char* g_scratch_dev[kMaxDevices];  // per device: its copy's address
+std::string g_setup_error;                   // why the last setup left no address
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -48,16 +50,32 @@ size_t layout(const Cfg& c, size_t off[5]) {
 
 }  // namespace
 
-int noalloc_setup(int device) {
-    if (device < 0 || device >= kMaxDevices)
-        return fail(HFMOE_ERR_UNSUPPORTED, "device %d: the no-allocation scratch covers devices 0..%d", device,
-                    kMaxDevices - 1);
-    if (g_scratch_dev[device]) return HFMOE_OK;
+// Never fails hfmoe_init: on any error the device's address stays null, the
+// reason is kept for the entry point's error message, and a sticky HIP error
+// is cleared so that it does not surface in the next, unrelated call.
+// HFMOE_NOALLOC_DISABLE=1 leaves the address unset on purpose (the entry
+// point then reports HFMOE_ERR_NOT_INITIALIZED).
+void noalloc_setup(int device) {
+    char why[160];
+    if (env_int("HFMOE_NOALLOC_DISABLE", 0)) {
+        g_setup_error = "disabled by HFMOE_NOALLOC_DISABLE";
+        return;
+    }
+    if (device < 0 || device >= kMaxDevices) {
+        snprintf(why, sizeof why, "device %d: the scratch covers devices 0..%d", device, kMaxDevices - 1);
+        g_setup_error = why;
+        return;
+    }
+    if (g_scratch_dev[device]) return;
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        snprintf(why, sizeof why, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_setup_error = why;
+        return;
+    }
     g_scratch_dev[device] = static_cast<unsigned char*>(p);
-    return HFMOE_OK;
 }
 
 }  // namespace hf
@@ -87,7 +105,9 @@ int hfmoe_moe_forward_noalloc(int layer, const float* x_dev, int32_t T, float* o
         return fail(HFMOE_ERR_UNSUPPORTED, "layer shape needs %zu bytes of scratch, more than the %zu available", need,
                     kScratchBytes);
     unsigned char* base = (g.device >= 0 && g.device < kMaxDevices) ? g_scratch_dev[g.device] : nullptr;
-    if (!base) return fail(HFMOE_ERR_NOT_INITIALIZED, "no-allocation scratch of device %d is not set up", g.device);
+    if (!base)
+        return fail(HFMOE_ERR_NOT_INITIALIZED, "no-allocation scratch of device %d is not set up (%s)", g.device,
+                    g_setup_error.empty() ? "unknown" : g_setup_error.c_str());
     const T1Buffers b{reinterpret_cast<float*>(base + off[0]), reinterpret_cast<float2*>(base + off[1]),
                       reinterpret_cast<int*>(base + off[2]), reinterpret_cast<float*>(base + off[3]),
                       reinterpret_cast<float*>(base + off[4])};

@@ -424,8 +424,8 @@ int hfmoe_stream_read_counters(hfmoe_stream_counters* out) {
     out->pred_wasted = n.pred_wasted;
     out->pred_resident = n.pred_resident;
     out->copies = n.copies;
-    out->pinned = n.pinned;
     out->slots = g.pool.slots;
+    out->pinned = n.pinned > (uint64_t)INT32_MAX ? INT32_MAX : (int32_t)n.pinned;
     return HFMOE_OK;
 }
 

@@ -242,10 +242,15 @@ typedef struct hfmoe_stream_counters {
     uint64_t pred_wasted;    /* copied-ahead experts evicted unused */
     uint64_t pred_resident;  /* predictions already resident (no copy) */
     uint64_t copies;         /* expert weight sets copied host -> HBM */
-    uint64_t pinned;         /* resident experts pinned by prob_resident */
     int32_t slots;           /* HBM slots in the pool (0 before the first streamed call) */
-    int32_t reserved;
-} hfmoe_stream_counters;
+    int32_t pinned;          /* resident experts pinned by prob_resident (saturates at INT32_MAX) */
+} hfmoe_stream_counters;     /* 72 bytes: pinned sits in what was the reserved field, so the
+                                layout and size are those of the first published header */
+#ifdef __cplusplus
+static_assert(sizeof(hfmoe_stream_counters) == 72, "hfmoe_stream_counters layout");
+#else
+_Static_assert(sizeof(hfmoe_stream_counters) == 72, "hfmoe_stream_counters layout");
+#endif
 
 int hfmoe_stream_set_options(const hfmoe_stream_options* opt);
 int hfmoe_stream_get_options(hfmoe_stream_options* opt);

@@ -56,7 +56,10 @@ def test_struct_layouts_match_header():
     assert C.sizeof(capi.KernelStat) == 32 + 8 + 8
     assert C.sizeof(capi.StreamOptions) == 4 * 8
     assert C.sizeof(capi.DenseWeights) == 8 * 4 + 4 * 2
-    assert C.sizeof(capi.StreamCounters) == 8 * 9 + 4 * 2
+    # The stream counters keep their first published layout: eight uint64
+    # counters, then slots and pinned (the latter in the former reserved field).
+    assert C.sizeof(capi.StreamCounters) == 8 * 8 + 4 * 2
+    assert capi.StreamCounters.slots.offset == 64 and capi.StreamCounters.pinned.offset == 68
 
 
 def test_calls_before_init_fail_loudly():
