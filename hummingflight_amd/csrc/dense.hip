@@ -10,10 +10,9 @@
 //   T > 1:  the grouped GEMM multiplies every token row by the one weight set
 //           (one group, no dispatch): gate/up with the SwiGLU epilogue into
 //           h (BF16 hi + lo), then down straight into out.  h stays exact to
-//           ~16 bits here: the dense down projection sums 12288 terms with
-//           weight 1, and an FP16 h (as the MoE layer's routed experts use)
-//           moves its outputs by up to ~4e-3 at hidden 6144, past the 2e-3
-//           absolute tolerance.
+//           ~16 bits, as in the MoE layer: the dense down projection sums
+//           12288 terms with weight 1, and an FP16 h moves its outputs by up
+//           to ~4e-3 at hidden 6144, past the 2e-3 absolute tolerance.
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 

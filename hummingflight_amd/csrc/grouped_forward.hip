@@ -51,7 +51,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.h16, w.y, w.part};
+                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -87,7 +87,6 @@ int grouped_workspace_alloc() {
         {(void**)&w.xl, 2 * (size_t)T * c.d},
         {(void**)&w.hh, 2 * R * c.I},
         {(void**)&w.hl, 2 * R * c.I},
-        {(void**)&w.h16, 2 * R * c.I},
         {(void**)&w.y, 4 * R * c.d},
         {(void**)&w.part, 4 * tks * c.E},
     };
@@ -184,28 +183,13 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
-    // Prefill tiles: the routed experts' h as FP16, which the down projection
-    // multiplies as one half (against FP16-converted weights); the shared
-    // expert's rows keep the BF16 hi / lo halves (its output enters with
-    // weight 1: FP16 there would take the worst output of a full-shape prefill
-    // to ~0.95 of the 2e-3 + 1e-2 tolerance, ~0.6 without it).  Should any
-    // FP16 value not fit, a second pass (which otherwise exits at once) writes
-    // the hi / lo halves of every row for the down projection to take instead.
-    // HFMOE_PREFILL_EXACT_H=1 keeps every row's h exact (the down projection's
-    // MFMA work and activation bytes doubled for the routed rows).
-    const bool f16_h = TR == kPrefillTileRows && env_int("HFMOE_PREFILL_EXACT_H", 0) == 0;
-    gu.h_f16 = f16_h ? w.h16 : nullptr;
-    gu.h_f16_bad = w.lo_flag + 1;
-    gu.f16_rows = P;  // the routed pairs; the shared expert's rows keep hi + lo
+    // h goes to the down projection exact, as BF16 hi + lo halves (about 16
+    // significand bits).  FP16 h (11 bits) was measured at 0.61 of the
+    // 2e-3 + 1e-2 tolerance over a full-shape prefill with near-uniform
+    // routing weights and past it (1.1-1.7) with a trained router's spread of
+    // weights or larger activations; the hi / lo halves stay at ~0.01-0.03.
     prof_begin(p, "expert_gateup_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "gate/up gemm");
-    if (gu.h_f16) {
-        GemmArgs hl = gu;
-        hl.h_f16 = nullptr;
-        hl.run_if = gu.h_f16_bad;
-        hl.item_ctr = nullptr;  // the counters are spent: static items
-        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, hl, gemm_blocks(TR), s), "gate/up hi/lo gemm");
-    }
 
     // Down projections of every group; row r's output lands at row perm[r] of
     // y: pair slot t*k + r for routed rows, T*k + t for the shared expert.
@@ -229,9 +213,6 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
-    dn.a_f16 = gu.h_f16;
-    dn.a_f16_bad = w.lo_flag + 1;
-    dn.f16_rows = P;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;

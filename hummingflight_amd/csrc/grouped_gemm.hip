@@ -46,27 +46,11 @@
 namespace hf {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef __fp16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int GBN = 128, GBK = kGemmTileK;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
-__device__ __forceinline__ f16x8_t as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8_t, v); }
-
-// Eight BF16 weights as FP16: widened to FP32 (exact), then packed with
-// round-toward-zero, which is exact too for every BF16 value of FP16's normal
-// range (8 significand bits into 11); smaller ones keep FP16's subnormal
-// spacing (6e-8).
-__device__ __forceinline__ f16x8_t bf16x8_to_f16x8(u32x4 v) {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v[i] << 16),
-                                                                         __uint_as_float(v[i] & 0xFFFF0000u)));
-    return __builtin_bit_cast(f16x8_t, r);
-}
 
 // 16-byte load through a global-address-space pointer.  Pointers read from
 // memory (the expert table) are generic; a generic load is a FLAT instruction,
@@ -230,9 +214,8 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
 // Stores one lane's share of a finished tile row gr: acc[cb][q] is output
 // column col0 + 16*cb + q (q = 0..3).  SWIGLU: blocks [0, NCB/2) are gate and
 // [NCB/2, NCB) the matching up columns; writes h = silu(g) * u
-// (glm_forward.cpp:444-446), 8 bytes per array: as FP16 alone when a.h_f16 is
-// given and gr < a.f16_rows (setting *a.h_f16_bad when a value does not fit
-// FP16), else as BF16 hi/lo.  PARTIAL / SCATTER: 16-byte FP32 stores (row stride N is a multiple
+// (glm_forward.cpp:444-446) as BF16 hi / lo halves, 8 bytes per array.
+// PARTIAL / SCATTER: 16-byte FP32 stores (row stride N is a multiple
 // of 4 whenever N is a multiple of 64; a ragged router width falls back to
 // single floats) to output row orow_idx (SCATTER: the token-order row of gr;
 // PARTIAL: gr).  NT: non-temporal stores.
@@ -241,7 +224,7 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                                                int ks, int orow_idx) {
     if (EPI == EPI_SWIGLU) {
         // h = silu(g) * u with the hardware exp2 and reciprocal (a few ulp of
-        // FP32): far below the rounding of h to FP16 or to a BF16 hi + lo pair.
+        // FP32): far below the rounding of h to a BF16 hi + lo pair.
         float hv[NCB / 2][4];
 #pragma unroll
         for (int cb = 0; cb < NCB / 2; ++cb)
@@ -250,26 +233,7 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                 const float gv = acc[cb][q];
                 hv[cb][q] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[cb + NCB / 2][q];
             }
-        bool bad = false;
-        if (a.h_f16 && gr < a.f16_rows) {  // FP16 h, one 8-byte store per column block
-            uint16_t* frow = a.h_f16 + (size_t)gr * a.N;
-#pragma unroll
-            for (int cb = 0; cb < NCB / 2; ++cb) {
-                const int col = col0 + 16 * cb;
-                if (col >= a.N) continue;  // N is a multiple of 64: 4 columns all in or all out
-                uint32_t fw[2];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t v0 = __builtin_bit_cast(uint16_t, (_Float16)hv[cb][q]);  // round to nearest even
-                    bad |= (v0 & 0x7C00u) == 0x7C00u;  // inf or NaN: h does not fit FP16
-                    if (q & 1)
-                        fw[q >> 1] |= v0 << 16;
-                    else
-                        fw[q >> 1] = v0;
-                }
-                *reinterpret_cast<uint2*>(frow + col) = make_uint2(fw[0], fw[1]);
-            }
-        } else {  // BF16 hi + lo halves
+        {  // BF16 hi + lo halves
             uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
             uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
 #pragma unroll
@@ -293,7 +257,6 @@ __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t 
                 *reinterpret_cast<uint2*>(lrow + col) = make_uint2(lw[0], lw[1]);
             }
         }
-        if (bad) *a.h_f16_bad = 1u;  // 0 -> 1 only, read by later kernels: a plain store
     } else {
         float* orow = EPI == EPI_PARTIAL ? a.out_f32 + ((size_t)ks * a.rows_total + orow_idx) * a.N
                                          : a.out_f32 + (size_t)orow_idx * a.N;
@@ -521,7 +484,6 @@ __device__ __forceinline__ bool group_absent(const GemmArgs& a, int g) {
 template <int EPI, int LOM, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void grouped_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) BStage ring[];  // kRingBytes
-    if (a.run_if && *a.run_if == 0u) return;
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar branches
 
@@ -592,14 +554,11 @@ static_assert(split_lds_max(192, 4) <= 160 * 1024 && split_lds_max(192, 6) <= 16
                   split_lds_max(256, 4) <= 160 * 1024,
               "LDS");
 
-// F16: A is the FP16 copy (a_f16, one half) and the weights are converted to
-// FP16 as they leave the LDS.
 // on_setup() runs once the item's own loads (tile table, row map) are out,
 // before its first DMA.
-template <int EPI, int ROWS, int HALVES, bool F16 = false, class Setup>
+template <int EPI, int ROWS, int HALVES, class Setup>
 __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
                                                 Setup&& on_setup) {
-    static_assert(!F16 || HALVES == 1, "the FP16 activations have one half");
     constexpr int CB = split_cb<EPI, ROWS>();
     constexpr int RBW = ROWS / 32;                 // row blocks per wavefront
     constexpr int AST = ROWS * GBK;                // elements per A stage
@@ -678,7 +637,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // Byte offsets within 4 GiB of each operand's base (every activation and
     // weight buffer of a layer is far smaller).
     const __amdgpu_buffer_rsrc_t rb = raw_rsrc(uniform_ptr((EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0));
-    const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(F16 ? a.a_f16 : a.a_hi);
+    const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(a.a_hi);
     const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
 
     f32x4_t acc[RBW][CB];
@@ -755,11 +714,6 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
                     for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
                 }
             }
-            [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
-            if constexpr (F16) {
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[kh][cb]);
-            }
 #pragma unroll
             for (int j = 0; j < NM; ++j) {
                 if (j + 1 < NM)
@@ -767,14 +721,9 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
                 else if (kh == 0)
                     av[1][0] = afrag(at, 0, 1);
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    if constexpr (F16)
-                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av[kh][j]), acc[j][cb],
-                                                                            0, 0, 0);
-                    else
-                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]),
-                                                                             as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
-                }
+                for (int cb = 0; cb < CB; ++cb)
+                    acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]), as_bf16x8(av[kh][j]),
+                                                                         acc[j][cb], 0, 0, 0);
             }
         }
     };
@@ -793,11 +742,6 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
             }
-            [[maybe_unused]] f16x8_t wf[F16 ? CB : 1];
-            if constexpr (F16) {
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) wf[cb] = bf16x8_to_f16x8(w[kh][cb]);
-            }
 #pragma unroll
             for (int j = 0; j < RBW; ++j) {
                 if (j < nm) {  // a guard, not a break: acc must stay in registers
@@ -807,14 +751,9 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
                         av[1][0] = afrag(at, 0, 1);
                     }
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        if constexpr (F16)
-                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb], as_f16x8(av[kh][j]), acc[j][cb],
-                                                                                0, 0, 0);
-                        else
-                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]),
-                                                                                 as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
-                    }
+                    for (int cb = 0; cb < CB; ++cb)
+                        acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            as_bf16x8(w[kh][cb]), as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
                 }
             }
         }
@@ -949,15 +888,11 @@ __device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange
 template <int EPI, int LOM, int ROWS>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t slds[];  // split_lds_max(ROWS, CB) bytes
-    if (a.run_if && *a.run_if == 0u) return;
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
     const ItemRange r = item_range<true>(a, m_tiles);
     const bool use_lo = LOM == kLoAlways || (LOM == kLoByFlag && *a.a_lo_flag != 0u);
-    // FP16 activations (an FP16 copy of h) for the MoE down projection.
-    constexpr bool F16_OK = EPI == EPI_SCATTER;
-    const bool use_f16 = F16_OK && a.a_f16 && *a.a_f16_bad == 0u;
     // One item, then a barrier: every wavefront is done with the LDS rings
     // before the next item's loads land in them.  (The item's own loads have
     // all landed; its stores need not have.)
@@ -965,14 +900,6 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
         if (group_absent(a, a.tile_group ? a.tile_group[item / a.ksplit / a.n_tiles] : 0)) {
             on_setup();
             return;
-        }
-        if constexpr (F16_OK) {
-            const int mt = item / a.ksplit / a.n_tiles;
-            if (use_f16 && (a.tile_row0 ? a.tile_row0[mt] : mt * ROWS) < a.f16_rows) {
-                gemm_item_split<EPI, ROWS, 1, true>(a, item, slds, t, wave, on_setup);
-                lds_barrier();
-                return;
-            }
         }
         if (LOM != kLoNone && use_lo)
             gemm_item_split<EPI, ROWS, 2>(a, item, slds, t, wave, on_setup);
@@ -1181,9 +1108,8 @@ hipError_t launch_combine(const float* wts, const float* y, int T, int k, int d,
 
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s) {
-    // flag[0]: x has a nonzero lo half (set below); flag[1]: an FP16 copy of h
-    // overflowed (set by the gate/up epilogue of the same forward).
-    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 2);
+    // flag[0]: x has a nonzero lo half (set below).
+    hipError_t e = launch(clear_u32_kernel, dim3(1), dim3(64), 0, s, flag, 1);
     if (e != hipSuccess) return e;
     size_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;

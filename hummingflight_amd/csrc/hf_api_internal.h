@@ -41,12 +41,11 @@ struct GroupedWorkspace {
     int* ntiles = nullptr;       // [1] M tiles in use
     int* chunk_hist = nullptr;   // [kDispatchMaxChunks, E] dispatch chunk counts / first slots
     unsigned* item_ctr = nullptr;  // [kItemCounters] prefill GEMM work counters (zeroed by the dispatch)
-    unsigned int* lo_flag = nullptr;  // [0] x has a nonzero BF16 lo half, [1] h overflowed FP16
+    unsigned int* lo_flag = nullptr;  // [0] x has a nonzero BF16 lo half
     uint16_t* xh = nullptr;      // [maxT, d] x BF16 hi (token order)
     uint16_t* xl = nullptr;      // [maxT, d] x BF16 lo
     uint16_t* hh = nullptr;      // [rows, I] h hi (sorted rows)
     uint16_t* hl = nullptr;      // [rows, I] h lo
-    uint16_t* h16 = nullptr;     // [rows, I] h as FP16 (prefill down projection)
     float* y = nullptr;          // [rows, d] expert outputs at pair slots, shared rows after
     float* part = nullptr;       // [ksplit, maxT, E] router split-K partials
     int max_tiles = 0;

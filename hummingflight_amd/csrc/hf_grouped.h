@@ -58,21 +58,6 @@ struct GemmArgs {
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
     unsigned* item_ctr;         // 8 zeroed per-XCD work counters (null: static items; see run_items_dynamic)
-    // FP16 activations (the down projection's h, prefill tiles): multiplied
-    // instead of a_hi / a_lo while *a_f16_bad == 0, against the weights
-    // converted to FP16 in registers.
-    const uint16_t* a_f16;
-    const unsigned* a_f16_bad;
-    // SWIGLU: h as FP16 rows [rows][N] instead of the hi / lo halves (when not
-    // null); *h_f16_bad is set when a value does not fit FP16 (then the
-    // consumer needs the hi / lo halves: see run_if).
-    uint16_t* h_f16;
-    unsigned* h_f16_bad;
-    // Rows [0, f16_rows) take the FP16 h (SWIGLU: written as FP16; down: the
-    // FP16 operand); later rows keep the BF16 hi / lo halves.  The MoE layer
-    // sets it to T * k, so the shared expert (weight 1 in the output, the
-    // largest share of FP16 rounding error) stays exact.  0: none.
-    int f16_rows;
     // Nonzero (one group, statically dealt items): the XCDs split the tiles
     // into by_ntile N groups x (XCDs / by_ntile) M groups, one block each,
     // and walk their block's items with M tiles fastest, so the workgroups of
@@ -80,10 +65,6 @@ struct GemmArgs {
     // L2.  Groups must divide evenly; else (XCDs) N groups and one M group,
     // when the N tiles divide; else the usual dealing.
     int by_ntile;
-    // When not null, the launch does nothing unless *run_if != 0 (a second
-    // gate/up pass that writes the BF16 hi / lo halves only after some h did
-    // not fit FP16).
-    const unsigned* run_if;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.

@@ -126,15 +126,19 @@ class DeviceLayer:
             for q in range(3):
                 ptrs[3 * e + q] = base + q * proj * 2
         self._ptrs = ptrs
-        w = capi.LayerWeights(self.router.ptr, self.bias_buf.ptr,
-                              self.shared[0].ptr if Is else None,
-                              self.shared[1].ptr if Is else None,
-                              self.shared[2].ptr if Is else None,
-                              C.cast(ptrs, C.c_void_p),
-                              self.norm.ptr if self.norm else None,
-                              capi.EXPERTS_HOST_PINNED if self.experts_on_host else capi.EXPERTS_DEVICE, 0)
+        self.weights = capi.LayerWeights(self.router.ptr, self.bias_buf.ptr,
+                                         self.shared[0].ptr if Is else None,
+                                         self.shared[1].ptr if Is else None,
+                                         self.shared[2].ptr if Is else None,
+                                         C.cast(ptrs, C.c_void_p),
+                                         self.norm.ptr if self.norm else None,
+                                         capi.EXPERTS_HOST_PINNED if self.experts_on_host else capi.EXPERTS_DEVICE, 0)
         self.layer_id = self.layer if self.register_as is None else self.register_as
-        capi.call("hfmoe_register_layer", self.layer_id, C.byref(w))
+        self.register()
+
+    def register(self) -> None:
+        """(Re-)register the layer, e.g. after its weights were changed in place."""
+        capi.call("hfmoe_register_layer", self.layer_id, C.byref(self.weights))
 
     def _dev(self, nbytes: int) -> capi.DeviceBuffer:
         b = capi.DeviceBuffer(nbytes)

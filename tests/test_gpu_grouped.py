@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 from hummingflight_amd import capi, synth
-from moe_harness import FULL, SMALL, DevView, Run, assert_close
+from moe_harness import FULL, SMALL, DevView, DeviceBackedLayer, Run, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -226,78 +226,6 @@ def test_grouped_full_shape_t2560(hf):
     r.free()
 
 
-def test_prefill_4096_uniform_routing(hf):
-    # Prefill chunk: near-uniform routing (bias ~N(0, 0.001)), ~128 rows per expert.
-    T, d, E = 4096, FULL["hidden"], FULL["n_experts"]
-    bias = O.fill_f32(E, 66, O.tensor_id(0, O.ROLE_BIAS), 0.0, 0.001)
-    r = Run(FULL, n_group=8, topk_group=4, seed=66, T=T, bias=bias)
-    x = synth.make_x_dev(T, d, seed=66)
-    res = r.forward(x, T)
-    counts = check_dispatch(res, E)
-    assert counts.sum() == T * FULL["top_k"]
-    check_selection(r, res, T)
-    check_vs_decode(r, x, res, range(7, T, 128), d)
-    xh = x.download(np.float32, T * d).reshape(T, d)
-    for t in (0, 2047, 4095):
-        r.check_token(xh[t], res, t)
-    x.free()
-    r.free()
-
-
-@pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
-def test_prefill_fp16_h_error_budget(hf, monkeypatch, fp32_x):
-    # Full-shape prefill (T = 4096, near-uniform routing): the routed experts'
-    # h reaches the down projection as FP16 (the shared expert's stays exact).
-    # Every one of the 25M outputs is compared with the same call keeping all
-    # h exact (HFMOE_PREFILL_EXACT_H=1, BF16 hi + lo, itself within ~1 % of the
-    # tolerance of the exact result), so the share of the 2e-3 + 1e-2 * |out|
-    # tolerance that FP16 rounding takes is measured over every output rather
-    # than a few tokens (FP16 h for the shared expert too: up to 0.95 of it).
-    T, d, E = 4096, FULL["hidden"], FULL["n_experts"]
-    bias = O.fill_f32(E, 66, O.tensor_id(0, O.ROLE_BIAS), 0.0, 0.001)
-    r = Run(FULL, n_group=8, topk_group=4, seed=66, T=T, bias=bias)
-    xh = O.make_x(T, d, 66).astype(np.float32)
-    if fp32_x:
-        rng = np.random.default_rng(7)
-        xh = (xh * (1.0 + np.float32(2.0 ** -10) * rng.standard_normal(xh.shape).astype(np.float32))).astype(np.float32)
-    x = capi.DeviceBuffer.of(xh)
-    fast = r.forward(x, T)
-    monkeypatch.setenv("HFMOE_PREFILL_EXACT_H", "1")
-    exact = r.forward(x, T)
-    assert np.array_equal(fast["idx"], exact["idx"])
-    ref = exact["out"].astype(np.float64)
-    ratio = np.abs(fast["out"] - ref) / (2e-3 + 1e-2 * np.abs(ref))
-    print(f"max share of the tolerance taken by FP16 h: {ratio.max():.3f}")
-    assert ratio.max() < 0.8, ratio.max()
-    for t in (5, 2050):  # the exact path against the oracle
-        r.check_token(xh[t], exact, t)
-    x.free()
-    r.free()
-
-
-def test_prefill_4096_zipf_hot_experts(hf):
-    # Prefill chunk with Zipf(1.1)-skewed routing: hot experts span several
-    # 192-row tiles, cold ones leave their one tile mostly empty.
-    with open(os.path.join(os.path.dirname(__file__), "golden", "zipf_bias_e256.json")) as fh:
-        zb = json.load(fh)
-    T, d, E = 4096, FULL["hidden"], FULL["n_experts"]
-    seed = zb["layer_seed"]
-    r = Run(FULL, n_group=8, topk_group=4, seed=seed, T=T, bias=np.array(zb["bias"], np.float32))
-    x = synth.make_x_dev(T, d, seed=seed)
-    res = r.forward(x, T)
-    counts = check_dispatch(res, E)
-    assert counts.max() > 2 * 192 and counts.min() < 96
-    check_selection(r, res, T)
-    hot = np.argsort(-counts)[:2]
-    rows = [t for t in range(T) if np.isin(res["idx"][t], hot).any()]
-    check_vs_decode(r, x, res, rows[:: max(1, len(rows) // 16)] + list(range(11, T, 256)), d)
-    xh = x.download(np.float32, T * d).reshape(T, d)
-    for t in (rows[0], rows[-1], 4095):
-        r.check_token(xh[t], res, t)
-    x.free()
-    r.free()
-
-
 def test_grouped_repeat_is_deterministic(hf):
     T, d = 37, SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=67, T=T)
@@ -364,15 +292,15 @@ def test_batched_decode_t64_zipf(hf):
     r.free()
 
 
-@pytest.mark.parametrize("w_std", [0.02, 4.0], ids=["fp16_h", "h_overflows_fp16"])
-def test_prefill_tiles_fp16_h_and_its_fallback(hf, w_std):
-    # Prefill tiles multiply h as FP16 in the down projection; when any value
-    # of h does not fit FP16 (weights ~N(0, 4): |h| ~ 3e4 typically, past
-    # 65504 in the tails) the gate/up epilogue flags it and the down projection
-    # takes the BF16 hi/lo halves instead.  Either way every token matches the
-    # oracle.  At that weight scale an output is a small residual of terms near
-    # 1e7, so FP32 summation order alone moves it by ~1e-5 of the token's
-    # largest output: the absolute floor is 1e-4 of that instead of 2e-3.
+@pytest.mark.parametrize("w_std", [0.02, 4.0], ids=["unit_h", "h_beyond_1e5"])
+def test_prefill_tiles_h_magnitudes(hf, w_std):
+    # Prefill tiles carry h into the down projection as BF16 hi + lo halves,
+    # whatever its magnitude: weights ~N(0, 4) put |h| at ~3e4 typically and
+    # past 1e5 in the tails (beyond FP16's range).  Either way every token
+    # matches the oracle.  At that weight scale an output is a small residual
+    # of terms near 1e7, so FP32 summation order alone moves it by ~1e-5 of
+    # the token's largest output: the absolute floor is 1e-4 of that instead
+    # of 2e-3.
     T, d = 1024, SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=90, T=T, w_std=w_std)
     x = synth.make_x_dev(T, d, seed=90)
@@ -389,5 +317,34 @@ def test_prefill_tiles_fp16_h_and_its_fallback(hf, w_std):
         ref = r.ref.combine(xh[t], ridx, rw).astype(np.float64)
         err = np.abs(res["out"][t] - ref)
         assert np.all(err <= 1e-2 * np.abs(ref) + 1e-4 * np.abs(ref).max()), f"token {t}: {err.max()}"
+    x.free()
+    r.free()
+
+
+def test_prefill_down_weight_outside_fp16_range(hf):
+    # Weights enter the prefill GEMMs as BF16, whatever their magnitude: a
+    # down weight of 2^17 (BF16 0x4800; FP16 tops out at 65504), planted in
+    # one expert and registered again, reaches the outputs of that expert's
+    # tokens exactly (a clamped weight would be off by half of an output of
+    # ~1e4), which match the oracle.
+    T, d, I = 1024, SMALL["hidden"], SMALL["inter"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=93, T=T)
+    e_hot, row, col = 5, 7, 11
+    proj = I * d
+    at = r.dev.experts.ptr + (e_hot * 3 * proj + 2 * proj + row * I + col) * 2
+    capi.call("hfmoe_memcpy_h2d", at, np.array([0x4800], np.uint16).ctypes.data, 2)
+    r.dev.register()
+    host = DeviceBackedLayer(r.spec, r.dev)
+    assert host.expert(e_hot)[2][row * I + col] == 0x4800
+    x = synth.make_x_dev(T, d, seed=93)
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    check_dispatch(res, SMALL["n_experts"])
+    on_hot = [t for t in range(T) if e_hot in res["idx"][t]]
+    assert on_hot
+    for t in on_hot[:6] + [0, T - 1]:
+        ref = host.combine(xh[t], res["idx"][t], res["w"][t])
+        assert_close(res["out"][t], ref, f"token {t}")
+    assert np.max(np.abs(res["out"][on_hot, row])) > 100.0  # the planted weight's share is there
     x.free()
     r.free()
