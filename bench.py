@@ -25,7 +25,10 @@ Other workloads of the same layer:
 Prints one JSON line: tokens/s as `value`, the dominant kernel's achieved rate
 against its roofline as `roofline` (durations from the kernels' own dispatch
 timestamps, recorded on the launch stream during a second pass of the timed
-steps), and the reference CPU path timed on this host as `cpu_baseline`.
+steps), and the reference CPU path timed on this host as `cpu_baseline`.  The
+default (decode) line also carries `configs`: the batched, prefill (BF16-valued
+and FP32 activations) and streamed-chain workloads, each timed in the same run
+with steps of its own (--no-configs leaves them out).
 
     python bench.py [--steps K] [--warmup W]
                     [--workload decode|batched|prefill|streamed|streamed_cached|streamed_prefill|dense|lm_head|load|plugin|copy]
@@ -422,8 +425,12 @@ def profiled_pass(step, steps: int) -> tuple[dict, float]:
     return capi.profile_read(), sec
 
 
-def run_grouped(args, workload: str) -> dict:
-    """Batched decode (T=64, Zipf routing) or a prefill chunk (T=4096)."""
+def run_grouped(args, workload: str, fp32_x: bool = False) -> dict:
+    """Batched decode (T=64, Zipf routing) or a prefill chunk (T=4096).
+
+    fp32_x: activations that are not BF16-valued (BF16 values scaled by
+    1 + 2^-10 N(0, 1), FP32 like the reference's RMSNorm output), which the
+    GEMMs take as BF16 hi + lo halves."""
     shape = synth.LayerShape(**FULL)
     if workload == "batched":
         T = 64
@@ -440,6 +447,11 @@ def run_grouped(args, workload: str) -> dict:
     capi.call("hfmoe_configure", shape.config(max_tokens=T))
     layer = synth.DeviceLayer(shape, layer=0, seed=seed, **layer_kw)
     x = synth.make_x_dev(T, shape.hidden, seed=seed)
+    if fp32_x:
+        xh = x.download(np.float32, T * shape.hidden)
+        xh *= 1.0 + np.float32(2.0 ** -10) * np.random.default_rng(seed).standard_normal(xh.size).astype(np.float32)
+        x.upload(xh)
+        routing += "; FP32 activations (BF16 values x (1 + 2^-10 N(0,1)))"
     out = capi.DeviceBuffer(T * shape.hidden * 4)
     idx = capi.DeviceBuffer(T * shape.top_k * 4)
     dbg = capi.RouteDebug(None, idx.ptr, None, None, None)
@@ -847,6 +859,35 @@ METRICS = {
 }
 
 
+def run_configs(args) -> dict:
+    """The north star's other configurations of the same full-shape layer,
+    timed in the default run beside the decode line: batched decode (T=64,
+    Zipf popularity), prefill (T=4096, BF16-valued and FP32 activations) and
+    the 8-layer streamed chain (T=1, experts from pinned host RAM).  Each
+    with steps of its own; no CPU legs (the reference runs every batch token
+    by token, so its rate per token is the decode line's cpu_baseline, per
+    layer for the chain)."""
+    import copy
+    runs = [("batched_t64_zipf", lambda a: run_grouped(a, "batched"), 40, 5),
+            ("prefill_t4096", lambda a: run_grouped(a, "prefill"), 10, 2),
+            ("prefill_t4096_fp32_x", lambda a: run_grouped(a, "prefill", fp32_x=True), 10, 2),
+            ("streamed_chain8", lambda a: run_streamed(a), 4, 1)]
+    out = {}
+    for name, fn, steps, warm in runs:
+        a = copy.copy(args)
+        a.steps, a.warmup, a.no_cpu_baseline = steps, warm, True
+        t0 = time.perf_counter()
+        r = fn(a)
+        keep = {"tokens_per_s": round(r["value"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps,
+                "warmup": warm, "wall_s": round(time.perf_counter() - t0, 1)}
+        for key in ("config", "roofline", "layer", "kernels", "pcie_bytes_per_token", "expert_cache"):
+            if key in r:
+                keep[key] = r[key]
+        out[name] = keep
+        print(f"{name}: {keep['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -873,6 +914,10 @@ def main() -> int:
     ap.add_argument("--load-experts", type=int, default=64,
                     help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="decode: leave out the batched, prefill and streamed-chain extras")
+    ap.add_argument("--fp32-x", action="store_true",
+                    help="batched / prefill: FP32 activations (not BF16-valued)")
     ap.add_argument("--decode-only", action="store_true",
                     help="decode: only the distinct-token steps (no same-token, host-contract or CPU legs), "
                          "for kernel traces")
@@ -895,6 +940,8 @@ def main() -> int:
         return 0
     if args.workload == "decode":
         res = run_decode(args)
+        if not (args.no_configs or args.decode_only):
+            res["configs"] = run_configs(args)
     elif args.workload == "dense":
         res = run_dense(args)
     elif args.workload == "lm_head":
@@ -904,7 +951,7 @@ def main() -> int:
     elif args.workload == "streamed_prefill":
         res = run_streamed_prefill(args)
     else:
-        res = run_grouped(args, args.workload)
+        res = run_grouped(args, args.workload, fp32_x=args.fp32_x)
     line = {"metric": METRICS[args.workload], "value": round(res.pop("value"), 2), "unit": "tokens/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(res.pop("ms_per_step"), 5), "higher_is_better": True, "scaling": "weak",
