@@ -694,24 +694,33 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // code: a guard per row block inside the K loop becomes a branch per
     // block, and the counter waits at the branches' joins fall back to
     // lgkmcnt(0), which serialises every fragment read with its multiplies.
-    auto compute_n = [&](const uint16_t* at, const uint16_t* bt, auto nm_c) {
+    // With two halves of A the weight fragments of a K stage are read once,
+    // in the hi sub-step, and kept in registers (wk) for the lo sub-step: the
+    // stage's ring slot is not refilled before the next stage's barrier, and
+    // the lo sub-step reads only its activations.
+    u32x4 wk[2][CB];
+    auto compute_n = [&](const uint16_t* at, const uint16_t* bt, auto nm_c, auto half_c) {
         constexpr int NM = decltype(nm_c)::value;
-        u32x4 w[2][CB];
+        constexpr bool READ_W = HALVES == 1 || decltype(half_c)::value == 0;
         u32x4 av[2][NM];
+        if constexpr (READ_W) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
+            for (int cb = 0; cb < CB; ++cb) wk[0][cb] = wfrag(bt, cb, 0);
+        }
         av[0][0] = afrag(at, 0, 0);
-        constexpr bool W1_EARLY = RBW * CB <= 24;  // registers permitting (not 384 columns or 256 rows)
-        if constexpr (W1_EARLY) {  // kh = 1's weights now too
+        // kh = 1's weights now too, registers permitting (not for 384 columns
+        // or 256 rows with one half, where they are read after kh = 0)
+        constexpr bool W1_EARLY = RBW * CB <= 24 || HALVES == 2;
+        if constexpr (READ_W && W1_EARLY) {
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
+            for (int cb = 0; cb < CB; ++cb) wk[1][cb] = wfrag(bt, cb, 1);
         }
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-            if constexpr (!W1_EARLY) {
+            if constexpr (READ_W && !W1_EARLY) {
                 if (kh == 1) {
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
+                    for (int cb = 0; cb < CB; ++cb) wk[1][cb] = wfrag(bt, cb, 1);
                 }
             }
 #pragma unroll
@@ -722,7 +731,7 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
                     av[1][0] = afrag(at, 0, 1);
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
-                    acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w[kh][cb]), as_bf16x8(av[kh][j]),
+                    acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wk[kh][cb]), as_bf16x8(av[kh][j]),
                                                                          acc[j][cb], 0, 0, 0);
             }
         }
@@ -730,15 +739,18 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     // The same with the row-block count known only at run time (a guard per
     // row block): for tiles whose accumulators leave no registers for a K
     // loop per row-block count (384 columns, or 256 rows).
-    auto compute_rt = [&](const uint16_t* at, const uint16_t* bt, int nm) {
-        u32x4 w[2][CB];
+    auto compute_rt = [&](const uint16_t* at, const uint16_t* bt, int nm, auto half_c) {
+        constexpr bool READ_W = HALVES == 1 || decltype(half_c)::value == 0;
+        u32x4 (&w)[2][CB] = wk;
         u32x4 av[2][RBW];
+        if constexpr (READ_W) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
+            for (int cb = 0; cb < CB; ++cb) w[0][cb] = wfrag(bt, cb, 0);
+        }
         av[0][0] = afrag(at, 0, 0);
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-            if (kh == 1) {
+            if (READ_W && kh == 1) {
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) w[1][cb] = wfrag(bt, cb, 1);
             }
@@ -759,7 +771,9 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         }
     };
     // One K loop per row-block count where registers allow it (192-row
-    // gate/up tiles: 96 accumulator registers), else one K loop with guards.
+    // gate/up tiles: 96 accumulator registers; any tile whose weight
+    // fragments serve two halves, as they need no second set of registers),
+    // else one K loop with guards.
     constexpr bool PER_NM = RBW * CB <= 24;
     auto substep = [&](int s, auto half_c, auto nm_c) {
         constexpr int half = decltype(half_c)::value;
@@ -783,14 +797,14 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         const uint16_t* at = aring + (j % RA) * AST;
         const uint16_t* bt = bring + (s % RB) * (64 * CB * GBK);
         if constexpr (!PER_NM)
-            compute_rt(at, bt, nm);
+            compute_rt(at, bt, nm, half_c);
         else if constexpr (decltype(nm_c)::value > 0)
-            compute_n(at, bt, nm_c);
+            compute_n(at, bt, nm_c, half_c);
     };
     // SCATTER: the token-order output rows of the epilogue, read now (192-row
     // tiles; the 256-row tiles have no registers to spare) so that their
     // latency hides under the item.
-    constexpr bool EARLY_ROWS = EPI == EPI_SCATTER && ROWS == kPrefillTileRows;
+    constexpr bool EARLY_ROWS = EPI == EPI_SCATTER && ROWS == kPrefillTileRows && HALVES == 1;
     [[maybe_unused]] int orow[EARLY_ROWS ? RBW : 1];
     if constexpr (EARLY_ROWS) {
 #pragma unroll
