@@ -183,6 +183,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.h_lo = w.hl;
     gu.ksplit = 1;
     gu.item_ctr = TR == kPrefillTileRows ? w.item_ctr : nullptr;  // short batched items: static
+    gu.shared_mtiles = (shared_rows + TR - 1) / TR;
     // h goes to the down projection exact, as BF16 hi + lo halves (about 16
     // significand bits).  FP16 h (11 bits) was measured at 0.61 of the
     // 2e-3 + 1e-2 tolerance over a full-shape prefill with near-uniform
@@ -213,6 +214,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
+    dn.shared_mtiles = gu.shared_mtiles;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;

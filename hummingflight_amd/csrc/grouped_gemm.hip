@@ -162,6 +162,20 @@ struct ItemRange {
     // [m0, m0 + m_cnt), M tiles fastest
     bool by_ntile;
     int n0, n_local, m0, m_cnt, ksplit;
+    // Dynamic by_mtile dealing with the shared expert's last sh_m M tiles
+    // dealt by blocks of sh_nl N tiles (GemmArgs::shared_mtiles; 0: none):
+    // XCD x's items are those sh_nl N tiles over the sh_m tiles, M fastest,
+    // then its routed M tiles x, x + nxcd, ... (ksplit 1).
+    int m_tiles, sh_m, sh_nl;
+    __device__ __forceinline__ int xcd_items(int x) const {
+        return (m_tiles - sh_m - x + nxcd - 1) / nxcd * per_m + sh_nl * sh_m;
+    }
+    __device__ __forceinline__ int xcd_item(int x, int li) const {
+        const int ns = sh_nl * sh_m;
+        if (li < ns) return (m_tiles - sh_m + li % sh_m) * per_m + x * sh_nl + li / sh_m;
+        li -= ns;
+        return (x + nxcd * (li / per_m)) * per_m + li % per_m;
+    }
     __device__ __forceinline__ int item(int li) const {
         if (by_ntile) {
             const int per_n = m_cnt * ksplit;
@@ -194,6 +208,11 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
         r.m0 = (r.xcd / gn) * r.m_cnt;
     }
     r.by_mtile = !r.by_ntile && DEAL_M && m_tiles >= r.nxcd;
+    r.m_tiles = m_tiles;
+    const bool sh = r.by_mtile && a.item_ctr && a.ksplit == 1 && a.shared_mtiles > 0 &&
+                    a.shared_mtiles <= m_tiles && a.n_tiles % r.nxcd == 0;
+    r.sh_m = sh ? a.shared_mtiles : 0;
+    r.sh_nl = sh ? a.n_tiles / r.nxcd : 0;
     const int local = blockIdx.x / r.nxcd;
     if (r.by_ntile) {
         r.begin = local;
@@ -876,8 +895,7 @@ __device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange
     auto settle = [&](int li) {
         for (;;) {
             const int x = (r.xcd + probe) % r.nxcd;
-            if (li < (m_tiles - x + r.nxcd - 1) / r.nxcd * r.per_m)
-                return (x + r.nxcd * (li / r.per_m)) * r.per_m + li % r.per_m;
+            if (li < r.xcd_items(x)) return r.xcd_item(x, li);
             if (++probe >= r.nxcd) return -1;
             li = grab();
         }

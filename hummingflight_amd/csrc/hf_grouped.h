@@ -65,6 +65,13 @@ struct GemmArgs {
     // L2.  Groups must divide evenly; else (XCDs) N groups and one M group,
     // when the N tiles divide; else the usual dealing.
     int by_ntile;
+    // M tiles of the last group (the shared expert's rows), when the prefill
+    // kernel takes dynamic items (item_ctr) with ksplit 1 and n_tiles a
+    // multiple of the XCD count: each XCD then takes the items of its block
+    // of n_tiles / 8 N tiles over all of these M tiles first, M tiles fastest,
+    // so that its workgroups stream each shared weight tile together through
+    // the XCD's L2 rather than once per M tile.  0: no such group.
+    int shared_mtiles;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.
