@@ -39,6 +39,7 @@
 #include "hf_api_internal.h"
 #include "hf_grouped.h"
 #include "hf_select.h"
+#include "item_deal.h"
 #include "split_pipeline.h"
 
 #include <type_traits>
@@ -162,20 +163,11 @@ struct ItemRange {
     // [m0, m0 + m_cnt), M tiles fastest
     bool by_ntile;
     int n0, n_local, m0, m_cnt, ksplit;
-    // Dynamic by_mtile dealing with the shared expert's last sh_m M tiles
-    // dealt by blocks of sh_nl N tiles (GemmArgs::shared_mtiles; 0: none):
-    // XCD x's items are those sh_nl N tiles over the sh_m tiles, M fastest,
-    // then its routed M tiles x, x + nxcd, ... (ksplit 1).
+    // Dynamic by_mtile dealing (item_deal.h), the shared expert's last
+    // sh_m M tiles dealt by blocks of sh_nl N tiles (GemmArgs::shared_mtiles;
+    // 0: none).
     int m_tiles, sh_m, sh_nl;
-    __device__ __forceinline__ int xcd_items(int x) const {
-        return (m_tiles - sh_m - x + nxcd - 1) / nxcd * per_m + sh_nl * sh_m;
-    }
-    __device__ __forceinline__ int xcd_item(int x, int li) const {
-        const int ns = sh_nl * sh_m;
-        if (li < ns) return (m_tiles - sh_m + li % sh_m) * per_m + x * sh_nl + li / sh_m;
-        li -= ns;
-        return (x + nxcd * (li / per_m)) * per_m + li % per_m;
-    }
+    __device__ __forceinline__ XcdDeal deal() const { return XcdDeal{m_tiles, per_m, nxcd, sh_m, sh_nl}; }
     __device__ __forceinline__ int item(int li) const {
         if (by_ntile) {
             const int per_n = m_cnt * ksplit;
@@ -895,7 +887,7 @@ __device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange
     auto settle = [&](int li) {
         for (;;) {
             const int x = (r.xcd + probe) % r.nxcd;
-            if (li < r.xcd_items(x)) return r.xcd_item(x, li);
+            if (li < xcd_items(r.deal(), x)) return xcd_item(r.deal(), x, li);
             if (++probe >= r.nxcd) return -1;
             li = grab();
         }

@@ -1,0 +1,40 @@
+"""Item dealing of the prefill grouped GEMM (item_deal.h, dynamic_items in
+grouped_gemm.hip): every (M tile, N tile) item is drawn exactly once over
+the XCDs' counters, the shared expert's M tiles by N blocks per XCD, first,
+M tiles fastest, and every other M tile whole by the XCD that owns it.
+Checked by brute force in a host build of the header (tests/item_deal) over
+the shapes the library launches (T = 4096 at d = 6144: 256 routed tiles + 22
+shared, 16 N tiles) and over random shapes, and with no shared group (the
+dealing before it: whole M tiles round-robin)."""
+import os
+import random
+import subprocess
+
+DRIVER_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "item_deal")
+
+
+def run_cases(cases):
+    subprocess.run(["make", "-s", "-C", DRIVER_DIR], check=True)
+    text = "".join(f"{m} {p} {x} {sm} {nl}\n" for m, p, x, sm, nl in cases)
+    r = subprocess.run([os.path.join(DRIVER_DIR, "driver")], input=text, capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip() == f"ok {len(cases)}"
+
+
+def test_dealing_of_the_benchmark_shapes():
+    # prefill T = 4096: 256 routed M tiles + 22 shared (192 rows), 16 N tiles
+    # for gate/up (128 h columns) and down (384 columns); a Zipf batch with
+    # multi-tile hot experts; no shared expert.
+    run_cases([(278, 16, 8, 22, 2), (300, 16, 8, 22, 2), (256, 16, 8, 0, 0), (9, 16, 8, 1, 2)])
+
+
+def test_dealing_of_random_shapes():
+    rng = random.Random(7)
+    cases = []
+    for _ in range(400):
+        nxcd = rng.choice([1, 2, 4, 8])
+        per_m = nxcd * rng.randint(1, 6)
+        m_tiles = rng.randint(nxcd, 400)
+        sh_m = rng.choice([0, rng.randint(1, min(m_tiles, 40))])
+        cases.append((m_tiles, per_m, nxcd, sh_m, per_m // nxcd if sh_m else 0))
+    run_cases(cases)
