@@ -869,16 +869,17 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
     }
 }
 
-// Dynamic items of the prefill kernel: each XCD's workgroups take the items of
-// the XCD's M tiles in order from a counter (zeroed by the dispatch), then help
-// the other XCDs with theirs, so the kernel ends when the last item does, not
+// Dynamic items of the prefill kernel: each XCD's workgroups take the XCD's
+// items (item_deal.h: its block of the shared expert's items, then its own M
+// tiles) in order from a counter (zeroed by the dispatch), then help the
+// other XCDs with theirs, so the kernel ends when the last item does, not
 // when the workgroup dealt the most items does.  Thread 0 takes the next item
 // while the current one runs (its atomic goes out with the item's first
 // loads), so no workgroup waits on the counter between items.  Every grab
 // advances a counter and each counter stops yielding at its XCD's item count:
 // the loop ends.
 template <class Run>
-__device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange& r, int m_tiles, Run&& run) {
+__device__ __forceinline__ void dynamic_items(const GemmArgs& a, const ItemRange& r, Run&& run) {
     const int t = threadIdx.x;
     __shared__ int next_item;
     int probe = 0;  // thread 0: counters found spent, in probing order from this XCD's
@@ -937,7 +938,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
         for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li), [] {});
         return;
     }
-    if constexpr (ROWS == kPrefillTileRows) dynamic_items(a, r, m_tiles, run);
+    if constexpr (ROWS == kPrefillTileRows) dynamic_items(a, r, run);
 }
 
 // out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):
