@@ -57,7 +57,7 @@ struct GemmArgs {
     uint16_t* h_lo;
     const int* scatter_rows;    // SCATTER: y row of GEMM row r
     int ksplit;                 // split-K factor (PARTIAL only; 1 otherwise)
-    unsigned* item_ctr;         // 8 zeroed per-XCD work counters (null: static items; see run_items_dynamic)
+    unsigned* item_ctr;         // 8 zeroed per-XCD work counters (null: static items; see dynamic_items)
     // Nonzero (one group, statically dealt items): the XCDs split the tiles
     // into by_ntile N groups x (XCDs / by_ntile) M groups, one block each,
     // and walk their block's items with M tiles fastest, so the workgroups of
