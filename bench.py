@@ -859,7 +859,7 @@ METRICS = {
 }
 
 
-def run_configs(args) -> dict:
+def run_configs(args, cpu_tokens_per_s: float | None = None) -> dict:
     """The north star's other configurations of the same full-shape layer,
     timed in the default run beside the decode line: batched decode (T=64,
     Zipf popularity), prefill (T=4096, BF16-valued and FP32 activations) and
@@ -883,6 +883,15 @@ def run_configs(args) -> dict:
         for key in ("config", "roofline", "layer", "kernels", "pcie_bytes_per_token", "expert_cache"):
             if key in r:
                 keep[key] = r[key]
+        if cpu_tokens_per_s:
+            # The reference runs a batch token by token (glm_forward.cpp:755), each token
+            # reading its 8 routed + 1 shared experts of equal size, so its rate per token
+            # is the decode line's; a token crosses all 8 layers of the chain.
+            layers = r.get("config", {}).get("layers", 1)
+            keep["cpu_baseline"] = {"value": round(cpu_tokens_per_s / layers, 2), "unit": "tokens/s",
+                                    "kind": "reference",
+                                    "sample": "the decode line's cpu_baseline per token"
+                                              + (f", over {layers} layers" if layers > 1 else "")}
         out[name] = keep
         print(f"{name}: {keep['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
     return out
@@ -941,7 +950,7 @@ def main() -> int:
     if args.workload == "decode":
         res = run_decode(args)
         if not (args.no_configs or args.decode_only):
-            res["configs"] = run_configs(args)
+            res["configs"] = run_configs(args, res.get("cpu_baseline", {}).get("value"))
     elif args.workload == "dense":
         res = run_dense(args)
     elif args.workload == "lm_head":
