@@ -86,6 +86,11 @@ def test_prefill_4096_uniform_every_output(layer66, fp32_x):
             np.float32)
     x = capi.DeviceBuffer.of(xh)
     res = r.forward(x, T)
+    # Workgroups draw GEMM items from counters in whatever order they arrive;
+    # every item is computed the same way wherever it runs: a second call is
+    # bit-identical.
+    again = r.forward(x, T)
+    assert np.array_equal(res["out"].view(np.uint32), again["out"].view(np.uint32))
     x.free()
     counts = check_routing(r, res)
     assert counts.sum() == T * K
