@@ -40,9 +40,10 @@ int gemm_blocks(int tile_rows) {
     return env_int("HFMOE_GEMM_BLOCKS", tile_rows == kGemmTileRows ? g.num_cus * 2 : g.num_cus);
 }
 
-// Prefill tiles (192 x 384) once experts average 96+ rows: an expert's rows
+// Prefill tiles (192 rows) once experts average 96+ rows: an expert's rows
 // then fit one tile, its weights stream through the memory system once, and
-// each activation row is requested once per 384 weight rows.
+// each activation row is requested once per 512 (gate/up, the wide tiles) or
+// 384 (down) weight rows.
 static int expert_tile_rows(int T) {
     const Cfg& c = g.cfg;
     return (size_t)T * c.k >= (size_t)96 * c.E ? kPrefillTileRows : kGemmTileRows;
@@ -110,6 +111,12 @@ int grouped_workspace_alloc() {
 
 int grouped_tile_rows(int T) { return expert_tile_rows(T); }
 
+// The prefill gate/up GEMM takes the wide tiles (512 weight rows, 256
+// outputs of h) unless HFMOE_PREFILL_WIDE=0 (256 weight rows): the down
+// projection keeps its 384-row tiles, on which its two halves of h cost fewer
+// LDS reads per weight byte.
+static bool prefill_wide() { return env_int("HFMOE_PREFILL_WIDE", 1) != 0; }
+
 int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     const Cfg& c = g.cfg;
     GroupedWorkspace& w = g.gws;
@@ -165,7 +172,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     gu.K = c.d;
     gu.N = c.I;
     gu.tile_rows = TR;
-    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU);
+    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU, c.I, prefill_wide());
     gu.n_tiles = gemm_n_tiles(EPI_SWIGLU, c.I, gu.tile_cols);
     gu.tile_group = w.tile_expert;
     gu.tile_row0 = w.tile_row0;

@@ -941,6 +941,284 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
     if constexpr (ROWS == kPrefillTileRows) dynamic_items(a, r, run);
 }
 
+// ---------------------------------------------------------------------------
+// Wide prefill gate/up tiles: 192 (M) x 512 (N: 256 gate + 256 up weight
+// rows) x 64 (K), eight wavefronts, one workgroup per CU.
+//
+// What bounds the prefill gate/up GEMM is the CU's stream of line requests to
+// L2: the weights once, plus the activation rows once per N tile.  Per weight
+// byte the activations add rows x halves / N; 512 weight rows per tile instead
+// of 256 cut that from 0.56 to 0.28 (BF16-valued x) and from 1.12 to 0.56
+// (FP32 x: hi and lo halves).  Registers and LDS set the layout:
+//   * wavefront w owns weight rows [64 w, 64 w + 64) of the tile (32 gate
+//     rows then the 32 matching up rows) and all 192 rows of the M tile:
+//     12 x 4 accumulator blocks, 192 of its 256 registers, and no weight
+//     fragment is read by two wavefronts;
+//   * so each wavefront streams its own weights, in 128-byte lines, through a
+//     private LDS ring of three half-stages (32 rows x 64 k, 4 KB) and copies
+//     a stage's fragments into 32 registers before multiplying it: the ring
+//     slots are free again right away, and 1.5 stages of weights stay in
+//     flight per wavefront with no barrier among wavefronts for them;
+//   * the activations (shared by all eight wavefronts) go by DMA into a
+//     two-slot ring of sub-steps (192 rows x 64 k; a K stage has one sub-step
+//     per half of A), with one barrier per sub-step.
+// 2 x 24 KB of activations + 8 x 3 x 4 KB of weights = 144 KB of LDS.
+// The cost of this layout is LDS reads: every wavefront reads all rows'
+// activation fragments, and with two halves of A its weight fragments twice
+// per stage (no registers are left to keep them), 6.5 bytes per weight byte
+// against 5 for the down projection's 384-row tiles, which therefore stay.
+constexpr int kWideWaves = 8;
+constexpr int kWideWaveRows = kWideTileCols / kWideWaves;  // weight rows per wavefront
+constexpr int kWideHalfRows = kWideWaveRows / 2;           // weight rows per half-stage
+constexpr int kWideWRing = 3;                              // half-stages per wavefront ring
+constexpr size_t kWideLds = 2 * (2 * (size_t)kPrefillTileRows * GBK +
+                                 (size_t)kWideWaves * kWideWRing * kWideHalfRows * GBK);
+static_assert(kWideLds + 64 <= 160 * 1024, "wide LDS");
+
+// Sub-step j = H * s + half multiplies A half `half` of K stage s.  Issue
+// order: sub-step j issues A(j + 1) after its barrier; the last sub-step of
+// stage s issues weight half-stages 2s + 3 and 2s + 4 (into the two ring
+// slots stage s came from, copied to registers by then).  Loads complete in
+// issue order, so the first sub-step of stage s, which needs A(j) and weight
+// half-stages 2s and 2s + 1, may leave exactly half-stage 2s + 2 (one
+// half-stage's DMAs) outstanding, and a second sub-step nothing.
+template <int HALVES, class Setup>
+__device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
+                                               Setup&& on_setup) {
+    constexpr int ROWS = kPrefillTileRows;
+    constexpr int AST = ROWS * GBK;                 // elements per A sub-step slot
+    constexpr int NAD = ROWS / 8 / kWideWaves;      // A DMAs (8 rows x 128 bytes) per wavefront per sub-step
+    constexpr int NWH = kWideHalfRows / 8;          // weight DMAs per half-stage
+    constexpr int WHS = kWideHalfRows * GBK;        // elements per weight half-stage slot
+    constexpr int CB = kWideWaveRows / 16;          // column blocks per wavefront
+    uint16_t* aring = lds;
+    uint16_t* wring = lds + 2 * AST + wave * (kWideWRing * WHS);
+    const int lane = t & 63;
+    const int fr = lane & 15;
+    const int fq = lane >> 4;
+    const int nk = a.K / GBK;
+    const int nj = nk * HALVES;
+
+    item = __builtin_amdgcn_readfirstlane(item);
+    const int nt = item % a.n_tiles;
+    const int mt = item / a.n_tiles;
+    // (the tile table is read with vector loads: the kernel writes memory too)
+    const int g = __builtin_amdgcn_readfirstlane(a.tile_group ? a.tile_group[mt] : 0);
+    const int row0 = __builtin_amdgcn_readfirstlane(a.tile_row0 ? a.tile_row0[mt] : mt * ROWS);
+    const int row_end = __builtin_amdgcn_readfirstlane(a.group_end ? a.group_end[g] : a.rows_total);
+    const int rows = min(ROWS, row_end - row0);
+    const int nrb = (rows + 15) >> 4;
+    const int n0 = nt * (kWideTileCols / 2);  // first h column of the tile
+    const uint16_t* b0 = a.b_tab ? a.b_tab[3 * g + a.b_which] : a.b_fixed0;      // gate rows
+    const uint16_t* b1 = a.b_tab ? a.b_tab[3 * g + a.b_which + 1] : a.b_fixed1;  // up rows
+
+    // DMA lane l of an 8-row block loads chunk (l & 7) ^ (l >> 3) of block row
+    // l >> 3, so 16-byte chunk c of slot row r sits at position c ^ (r & 7):
+    // conflict-free for the lane-contiguous DMA writes and for the fragment
+    // reads (16 rows x 16 bytes per quarter wavefront).
+    const int dr = lane >> 3;
+    const int dc = (lane & 7) ^ dr;
+    // A: 8-row block 4 i + wave of the tile (rows past the item's last re-read
+    // it; blocks past its last 16-row block are not loaded at all).
+    uint32_t aoff[NAD];
+#pragma unroll
+    for (int i = 0; i < NAD; ++i) {
+        const int r = 8 * (kWideWaves * i + wave) + dr;
+        const int gr = row0 + min(r, rows - 1);
+        const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
+        aoff[i] = (uint32_t)(2 * (src * a.K + dc * 8));
+    }
+    // Weights: half-stage h of this wavefront is gate rows (h = 0) or the
+    // matching up rows (h = 1) n0 + 32 w + [0, 32); DMA i covers 8 of them.
+    const int wrow = n0 + kWideHalfRows * wave + dr;
+    const uint32_t woff = (uint32_t)(2 * ((size_t)wrow * a.b_ld + dc * 8));
+    const __amdgpu_buffer_rsrc_t rw0 = raw_rsrc(uniform_ptr(b0));
+    const __amdgpu_buffer_rsrc_t rw1 = raw_rsrc(uniform_ptr(b1));
+    const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(a.a_hi);
+    const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
+    const uint32_t wrow_bytes = (uint32_t)a.b_ld * 2;
+
+    // DMA i of A sub-step j (nothing past the last sub-step or the item's rows).
+    auto issue_a1 = [&](int j, int i, int nab) {
+        const int blk = kWideWaves * i + wave;
+        if (j >= nj || blk >= nab) return;
+        const __amdgpu_buffer_rsrc_t ra = (j % HALVES) ? ra1 : ra0;
+        dma16<0>(ra, aoff[i], (uint32_t)(j / HALVES) * (2 * GBK), aring + (j & 1) * AST + blk * 512);
+    };
+    auto issue_a = [&](int j, int nab) {
+#pragma unroll
+        for (int i = 0; i < NAD; ++i) issue_a1(j, i, nab);
+    };
+    // DMA i of weight half-stage q = 2 s + h (nothing past the last).
+    auto issue_w1 = [&](int q, int i) {
+        if (q >= 2 * nk) return;
+        const int s = q >> 1, h = q & 1;
+        dma16(h ? rw1 : rw0, woff, (uint32_t)s * (2 * GBK) + (uint32_t)(8 * i) * wrow_bytes,
+              wring + (q % kWideWRing) * WHS + i * 512);
+    };
+    auto issue_w = [&](int q) {
+#pragma unroll
+        for (int i = 0; i < NWH; ++i) issue_w1(q, i);
+    };
+    // Fragments: slot row r, 16-byte chunk c at position c ^ (r & 7).
+    auto frag = [&](const uint16_t* slot, int r, int c) {
+        return *reinterpret_cast<const u32x4*>(slot + r * GBK + ((c ^ (r & 7)) * 8));
+    };
+
+    on_setup();
+    const int nab0 = 2 * nrb;
+    issue_a(0, nab0);
+    issue_w(0);
+    issue_w(1);
+    issue_w(2);
+
+    // The K loop, compiled per row-block count of the item (all four
+    // wavefronts share it), so every sub-step's multiplies are straight code.
+    auto kloop = [&](auto nm_c) __attribute__((always_inline)) {
+        constexpr int NM = decltype(nm_c)::value;
+        f32x4_t acc[NM > 0 ? NM : 1][CB];
+#pragma unroll
+        for (int j = 0; j < NM; ++j)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) acc[j][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        // One sub-step's multiplies: per k half, the CB weight fragments of
+        // that half (read from the wavefront's ring; the second half's reads
+        // go out one by one as the first half's last multiplies free their
+        // registers), each activation fragment (read one step ahead) against
+        // them.  The DMAs go out one at a time between row blocks rather than
+        // in a burst (a DMA waits at issue while the CU's queue of line
+        // requests is full, holding up the multiplies behind it): A(j + 1)
+        // over the first k half; in a stage's last sub-step (LAST), weight
+        // half-stages 2s + 3 and 2s + 4 over the second, once every read of
+        // the ring slots they overwrite has landed.
+        auto compute = [&](const uint16_t* at, int s, bool last, int jn, int nab) __attribute__((always_inline)) {
+            const uint16_t* w0 = wring + ((2 * s) % kWideWRing) * WHS;
+            const uint16_t* w1 = wring + ((2 * s + 1) % kWideWRing) * WHS;
+            auto wfrag = [&](int cb, int kh) {
+                return frag(cb < CB / 2 ? w0 : w1, 16 * (cb % (CB / 2)) + fr, kh * 4 + fq);
+            };
+            auto dma = [&](auto&& f) {
+                asm volatile("" ::: "memory");
+                f();
+                asm volatile("" ::: "memory");
+            };
+            // After row block r of k half kh (r == -1: before any).
+            auto dmas_after = [&](int kh, int r) {
+                constexpr int NMX = NM > 0 ? NM : 1;
+                if (kh == 0) {  // A(jn): DMA r + 1 after row block r, the rest after the last
+#pragma unroll
+                    for (int i = 0; i < NAD; ++i)
+                        if (i == r + 1 || (r == NMX - 1 && i > r + 1)) dma([&] { issue_a1(jn, i, nab); });
+                } else if (last) {  // 2 NWH weight DMAs spread over the row blocks
+                    if (r == -1) {
+                        asm volatile("" ::: "memory");
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slots' reads are done
+                    }
+#pragma unroll
+                    for (int k = 0; k < 2 * NWH; ++k)
+                        if (k * NMX / (2 * NWH) == r + 1 || (r == NMX - 1 && k * NMX / (2 * NWH) > r))
+                            dma([&] { issue_w1(2 * s + 3 + k / NWH, k % NWH); });
+                }
+            };
+            if constexpr (NM > 0) {
+                u32x4 wk[2][CB];  // [k half][column block]
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) wk[0][cb] = wfrag(cb, 0);
+                u32x4 av[2][NM];
+                av[0][0] = frag(at, fr, fq);
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh) {
+                    dmas_after(kh, -1);
+#pragma unroll
+                    for (int j = 0; j < NM; ++j) {
+                        if (j + 1 < NM)
+                            av[kh][j + 1] = frag(at, 16 * (j + 1) + fr, kh * 4 + fq);
+                        else if (kh == 0)
+                            av[1][0] = frag(at, fr, 4 + fq);
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) {
+                            acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                as_bf16x8(wk[kh][cb]), as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
+                            if (kh == 0 && j == NM - 1) wk[1][cb] = wfrag(cb, 1);
+                        }
+                        dmas_after(kh, j);
+                        // Keep the reads one step ahead: hoisted further, they
+                        // would hold registers the accumulators need.
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            } else {
+                issue_a(jn, nab);
+                if (last) {
+                    issue_w(2 * s + 3);
+                    issue_w(2 * s + 4);
+                }
+            }
+        };
+        for (int j = 0; j < nj; ++j) {
+            // Sub-step j: A(j); the first of a stage also weight half-stages
+            // 2s, 2s+1 (a second one waits for everything).
+            const int s = j / HALVES;
+            const bool first = HALVES == 1 || (j & 1) == 0;
+            if (first && s + 1 < nk)
+                wait_vmcnt<NWH>();
+            else
+                wait_vmcnt<0>();
+            lds_barrier();
+            int nab = nab0;
+            asm volatile("" : "+s"(nab));
+            compute(aring + (j & 1) * AST, s, HALVES == 1 || !first, j + 1, nab);
+        }
+        // Every load of the item has landed (the last stage waits for all).
+        // h columns n0 + 32 w + 16 cb + 4 fq + q from gate block cb and up block cb + 2.
+        const int col0 = n0 + kWideHalfRows * wave + 4 * fq;
+#pragma unroll
+        for (int j = 0; j < NM; ++j) {
+            const int rl = 16 * j + fr;
+            if (rl < rows) store_tile_row<EPI_SWIGLU, CB>(a, acc[j], row0 + rl, col0, 0, row0 + rl);
+        }
+    };
+    // Row-block counts in buckets (8 .. 12 exact, the near-uniform prefill's
+    // range; smaller ones rounded up to even): the extra blocks multiply rows
+    // that were not loaded and are never stored.
+    const int nb = nrb >= 8 ? nrb : (nrb + 1) & ~1;
+    static_for_desc<ROWS / 16>([&](auto n_c) {
+        constexpr int NM = decltype(n_c)::value;
+        if constexpr (NM >= 8 || NM % 2 == 0) {
+            if (nb == NM) kloop(std::integral_constant<int, NM>{});
+        }
+    });
+}
+
+// x (BF16 hi, and lo when the device flag says x is not BF16-valued) times
+// the gate and up weights, h = silu(g) * u out as BF16 hi / lo.
+__global__ __launch_bounds__(64 * kWideWaves, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t wlds[];  // kWideLds bytes
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
+    const ItemRange r = item_range<true>(a, m_tiles);
+    const bool use_lo = *a.a_lo_flag != 0u;
+    // One item, then a barrier: every wavefront is done with the activation
+    // ring before the next item's loads land in it.
+    auto run = [&](int item, auto&& on_setup) __attribute__((always_inline)) {
+        if (group_absent(a, a.tile_group ? a.tile_group[item / a.n_tiles] : 0)) {
+            on_setup();
+            return;
+        }
+        if (use_lo)
+            gemm_item_wide<2>(a, item, wlds, t, wave, on_setup);
+        else
+            gemm_item_wide<1>(a, item, wlds, t, wave, on_setup);
+        lds_barrier();
+    };
+    if (!a.item_ctr || !r.by_mtile) {
+        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li), [] {});
+        return;
+    }
+    dynamic_items(a, r, run);
+}
+
 // out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):
 // the weighted merge in rank order, then the shared expert (glm_forward.cpp:639-640, 658-660).
 __global__ void combine_kernel(const float* __restrict__ wts, const float* __restrict__ y, int T, int k,
@@ -1092,8 +1370,28 @@ static hipError_t launch_gemm_split(const GemmArgs& a, int blocks, hipStream_t s
     return launch(grouped_gemm_split_kernel<EPI, LOM, ROWS>, dim3(blocks), dim3(512), (uint32_t)lds, s, a);
 }
 
+static hipError_t launch_gemm_wide(const GemmArgs& a, int blocks, hipStream_t s) {
+    static bool raised = false;
+    if (!raised) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLds);
+        if (e != hipSuccess) return e;
+        raised = true;
+    }
+    return launch(grouped_gemm_wide_kernel, dim3(blocks), dim3(64 * kWideWaves), (uint32_t)kWideLds, s, a);
+}
+
 template <int EPI, int LOM>
 static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
+    if (a.tile_rows == kPrefillTileRows && a.tile_cols == kWideTileCols) {
+        // The MoE gate/up GEMM only (on x, whose lo half goes by the device
+        // flag), whole wide tiles (their weight DMAs are not clamped at N),
+        // one K split.
+        if constexpr (EPI == EPI_SWIGLU && LOM == kLoByFlag) {
+            if (a.N % (kWideTileCols / 2) == 0 && a.ksplit == 1 && a.a_lo_flag) return launch_gemm_wide(a, blocks, s);
+        }
+        return hipErrorInvalidValue;
+    }
     if (a.tile_rows == 192 && a.tile_cols == 64 * split_cb<EPI, 192>()) return launch_gemm_split<EPI, LOM, 192>(a, blocks, s);
     if (a.tile_rows == 256 && a.tile_cols == 64 * split_cb<EPI, 256>()) return launch_gemm_split<EPI, LOM, 256>(a, blocks, s);
     if (a.tile_rows == kGemmTileRows && a.tile_cols == GBN) return launch_gemm<EPI, LOM, 4>(a, blocks, s);

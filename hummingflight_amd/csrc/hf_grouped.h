@@ -13,12 +13,20 @@ constexpr int kGemmTileK = 64;      // K per pipeline stage (K % (64 * ksplit) =
 
 enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 
-// Weight rows per tile for M tiles of tile_rows rows (MoE prefill: 256 for
-// gate/up, i.e. 128 gate + 128 up rows, and 384 otherwise; one-group GEMMs
-// with 256-row tiles: 256), and the N tiles that cover N output columns (a
-// SWIGLU tile's weight rows are half gate, half up).
-inline int gemm_tile_cols(int tile_rows, int epi) {
-    if (tile_rows == kPrefillTileRows) return epi == EPI_SWIGLU ? 256 : 384;
+// Weight rows per tile of the wide prefill gate/up kernel (eight wavefronts
+// of 64 weight rows, 32 gate + 32 up, each over all 192 rows of an M tile).
+constexpr int kWideTileCols = 512;
+
+// Weight rows per tile for M tiles of tile_rows rows (MoE prefill: gate/up
+// 512 with wide = true when the N outputs of h divide into whole wide tiles,
+// else 256, i.e. 128 gate + 128 up rows; otherwise 384; one-group GEMMs with
+// 256-row tiles: 256), and the N tiles that cover N output columns (a SWIGLU
+// tile's weight rows are half gate, half up).
+inline int gemm_tile_cols(int tile_rows, int epi, int N = 0, bool wide = false) {
+    if (tile_rows == kPrefillTileRows) {
+        if (epi == EPI_SWIGLU) return wide && N > 0 && N % (kWideTileCols / 2) == 0 ? kWideTileCols : 256;
+        return 384;
+    }
     return tile_rows == kDenseTileRows ? 256 : 128;
 }
 inline int gemm_n_tiles(int epi, int N, int tile_cols) {

@@ -1,8 +1,9 @@
 """Full-shape prefill (T = 4096, d = 6144, 256 experts top-8 + 1 shared) checked
 over every output.
 
-The prefill chunk runs the 192-row MFMA grouped GEMMs, h entering the down
-projection as BF16 hi + lo halves.  Each batch is checked three ways:
+The prefill chunk runs the 192-row MFMA grouped GEMMs (512 weight rows per
+item), h entering the down projection as BF16 hi + lo halves.  Each batch is
+checked three ways:
   * dispatch offsets and permutation bit-exact with the oracle's stable
     counting sort, every token's selection and routing weights bit-exact with
     the oracle's given the GPU's router logits;
@@ -13,7 +14,8 @@ projection as BF16 hi + lo halves.  Each batch is checked three ways:
     near-uniform routing and 1.1-1.7 with skewed weights);
   * a token of every M tile of the dispatch (every routed expert's tiles,
     all of a hot expert's and all 22 of the shared expert's) against the
-    oracle's own moeLayer restatement.
+    oracle's own moeLayer restatement;
+  * (uniform and Zipf) bit for bit against the narrower 256 / 384-row tiles.
 
 Routing: near-uniform (bias ~N(0, 0.001)), with BF16-valued and with FP32
 activations; skewed routing weights (a trained router's spread: tokens with
@@ -74,8 +76,18 @@ def check_tiles_against_oracle(host, xh, res, what):
         assert_close(res["out"][t], ref, f"{what}: token {t}")
 
 
+def narrow_tiles_agree(r, x, res, monkeypatch):
+    # The wide tiles (512 weight rows per item) accumulate every output in the
+    # same order as the narrower ones (256 gate/up, 384 down weight rows;
+    # HFMOE_PREFILL_WIDE=0): K stage by stage, k half 0 then 1, hi then lo.
+    monkeypatch.setenv("HFMOE_PREFILL_WIDE", "0")
+    narrow = r.forward(x, T)
+    monkeypatch.delenv("HFMOE_PREFILL_WIDE")
+    assert np.array_equal(res["out"].view(np.uint32), narrow["out"].view(np.uint32)), "wide and narrow tiles differ"
+
+
 @pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
-def test_prefill_4096_uniform_every_output(layer66, fp32_x):
+def test_prefill_4096_uniform_every_output(layer66, fp32_x, monkeypatch):
     # Config 4: near-uniform routing, ~128 rows per expert, every routing
     # weight ~2.5 / 8.
     r, host = layer66
@@ -91,6 +103,7 @@ def test_prefill_4096_uniform_every_output(layer66, fp32_x):
     # bit-identical.
     again = r.forward(x, T)
     assert np.array_equal(res["out"].view(np.uint32), again["out"].view(np.uint32))
+    narrow_tiles_agree(r, x, res, monkeypatch)
     x.free()
     counts = check_routing(r, res)
     assert counts.sum() == T * K
@@ -141,7 +154,7 @@ def test_prefill_4096_skewed_routing_weights(layer66):
         assert_close(res["out"][t], host.combine(xh[t], res["idx"][t], res["w"][t]), f"token {t}")
 
 
-def test_prefill_4096_zipf_every_output(hf):
+def test_prefill_4096_zipf_every_output(hf, monkeypatch):
     # Zipf(1.1)-skewed expert popularity: hot experts span several 192-row
     # tiles, cold ones leave their one tile mostly empty.  (Reconfigures the
     # library: runs after the tests on the shared layer.)
@@ -153,6 +166,7 @@ def test_prefill_4096_zipf_every_output(hf):
     xh = O.make_x(T, D, seed).astype(np.float32)
     x = capi.DeviceBuffer.of(xh)
     res = r.forward(x, T)
+    narrow_tiles_agree(r, x, res, monkeypatch)
     x.free()
     counts = check_routing(r, res)
     assert counts.max() > 2 * TILE and counts.min() < 96
