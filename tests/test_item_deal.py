@@ -4,7 +4,8 @@ the XCDs' counters, the shared expert's M tiles by N blocks per XCD, first,
 M tiles fastest, and every other M tile whole by the XCD that owns it.
 Checked by brute force in a host build of the header (tests/item_deal) over
 the shapes the library launches (T = 4096 at d = 6144: 256 routed tiles + 22
-shared, 16 N tiles) and over random shapes, and with no shared group (the
+shared; gate/up 8 N tiles of 512 weight rows, down 16 of 384) and over random
+shapes, and with no shared group (the
 dealing before it: whole M tiles round-robin)."""
 import os
 import random
@@ -22,10 +23,11 @@ def run_cases(cases):
 
 
 def test_dealing_of_the_benchmark_shapes():
-    # prefill T = 4096: 256 routed M tiles + 22 shared (192 rows), 16 N tiles
-    # for gate/up (128 h columns) and down (384 columns); a Zipf batch with
-    # multi-tile hot experts; no shared expert.
-    run_cases([(278, 16, 8, 22, 2), (300, 16, 8, 22, 2), (256, 16, 8, 0, 0), (9, 16, 8, 1, 2)])
+    # prefill T = 4096: 256 routed M tiles + 22 shared (192 rows), 8 N tiles
+    # for gate/up (256 h columns) and 16 for down (384 columns); a Zipf batch
+    # with multi-tile hot experts; no shared expert.
+    run_cases([(278, 8, 8, 22, 1), (278, 16, 8, 22, 2), (300, 8, 8, 22, 1), (300, 16, 8, 22, 2),
+               (256, 16, 8, 0, 0), (9, 16, 8, 1, 2)])
 
 
 def test_dealing_of_random_shapes():
