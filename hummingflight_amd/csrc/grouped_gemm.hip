@@ -955,10 +955,12 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
 //     12 x 4 accumulator blocks, 192 of its 256 registers, and no weight
 //     fragment is read by two wavefronts;
 //   * so each wavefront streams its own weights, in 128-byte lines, through a
-//     private LDS ring of three half-stages (32 rows x 64 k, 4 KB) and copies
-//     a stage's fragments into 32 registers before multiplying it: the ring
-//     slots are free again right away, and 1.5 stages of weights stay in
-//     flight per wavefront with no barrier among wavefronts for them;
+//     private LDS ring of three half-stages (32 rows x 64 k, 4 KB), reading a
+//     k half's weight fragments into registers before multiplying with them;
+//     a stage's last sub-step refills the two slots it read with the next
+//     half-stages as soon as its first k half is done, so 1.5 stages of
+//     weights stay in flight per wavefront with no barrier among wavefronts
+//     for them;
 //   * the activations (shared by all eight wavefronts) go by DMA into a
 //     two-slot ring of sub-steps (192 rows x 64 k; a K stage has one sub-step
 //     per half of A), with one barrier per sub-step.
@@ -976,12 +978,13 @@ constexpr size_t kWideLds = 2 * (2 * (size_t)kPrefillTileRows * GBK +
 static_assert(kWideLds + 64 <= 160 * 1024, "wide LDS");
 
 // Sub-step j = H * s + half multiplies A half `half` of K stage s.  Issue
-// order: sub-step j issues A(j + 1) after its barrier; the last sub-step of
-// stage s issues weight half-stages 2s + 3 and 2s + 4 (into the two ring
-// slots stage s came from, copied to registers by then).  Loads complete in
-// issue order, so the first sub-step of stage s, which needs A(j) and weight
-// half-stages 2s and 2s + 1, may leave exactly half-stage 2s + 2 (one
-// half-stage's DMAs) outstanding, and a second sub-step nothing.
+// order: sub-step j issues A(j + 1) over its first k half (after its
+// barrier); the last sub-step of stage s issues weight half-stages 2s + 3 and
+// 2s + 4 over its second k half (into the two ring slots stage s came from,
+// whose reads have all landed by then).  Loads complete in issue order, so
+// the first sub-step of stage s, which needs A(j) and weight half-stages 2s
+// and 2s + 1, may leave exactly half-stage 2s + 2 (one half-stage's DMAs)
+// outstanding, and a second sub-step nothing.
 template <int HALVES, class Setup>
 __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
                                                Setup&& on_setup) {
