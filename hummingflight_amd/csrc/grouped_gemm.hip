@@ -992,6 +992,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     constexpr int AST = ROWS * GBK;                 // elements per A sub-step slot
     constexpr int NAD = ROWS / 8 / kWideWaves;      // A DMAs (8 rows x 128 bytes) per wavefront per sub-step
     constexpr int NWH = kWideHalfRows / 8;          // weight DMAs per half-stage
+    static_assert(NAD == 3 && NWH == 4, "the counts tests/split_pipeline checks the waits with");
     constexpr int WHS = kWideHalfRows * GBK;        // elements per weight half-stage slot
     constexpr int CB = kWideWaveRows / 16;          // column blocks per wavefront
     uint16_t* aring = lds;
@@ -1163,8 +1164,10 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
             // 2s, 2s+1 (a second one waits for everything).
             const int s = j / HALVES;
             const bool first = HALVES == 1 || (j & 1) == 0;
-            if (first && s + 1 < nk)
-                wait_vmcnt<NWH>();
+            if (!first)
+                wait_vmcnt<wide_after(1, NWH)>();
+            else if (wide_steady(s, nk))
+                wait_vmcnt<wide_after(0, NWH)>();
             else
                 wait_vmcnt<0>();
             lds_barrier();

@@ -1,7 +1,8 @@
 // split_pipeline.h -- prefetch depths, LDS sizes and wait counts of the
-// prefill grouped GEMM's two DMA rings (grouped_gemm_split_kernel).  Plain
-// constexpr C++ so a host build can check the wait counts against a
-// brute-force count of the issue sequence.
+// prefill grouped GEMMs' DMA rings (grouped_gemm_split_kernel, and the wait
+// counts of grouped_gemm_wide_kernel at the end).  Plain constexpr C++ so a
+// host build can check the wait counts against a brute-force count of the
+// issue sequence.
 //
 // Per item, sub-step j = H * s + half multiplies A half `half` (H = 2 when the
 // activations carry a lo half) of K stage s against B stage s.  A is DA
@@ -55,5 +56,18 @@ constexpr bool split_a_may_skip(int H, int DA, int DB, int NAD, int NBD) {
         if (split_after(H, DA, DB, half, NAD, NBD) != split_after(H, DA, DB, half, 0, NBD)) return false;
     return true;
 }
+
+// Wide gate/up tiles (grouped_gemm_wide_kernel): per wavefront, a prologue
+// issues A(0) and weight half-stages 0, 1, 2; sub-step j = H*s + half waits,
+// meets the workgroup at a barrier, issues A(j + 1) (0 .. NAD DMA
+// instructions: the item's used rows) and, on a stage's last sub-step, weight
+// half-stages 2s + 3 and 2s + 4 (NWH each); loads past the item issue
+// nothing.  The first sub-step of stage s needs A(j) and half-stages 2s and
+// 2s + 1, a second sub-step A(j).  Steady count of DMA instructions a
+// sub-step may leave outstanding:
+constexpr int wide_after(int half, int nwh) { return half == 0 ? nwh : 0; }
+// ... valid while the loads it assumes were issued (half-stage 2s + 2
+// exists); otherwise the sub-step waits for everything.
+constexpr bool wide_steady(int s, int nk) { return s + 1 < nk; }
 
 }  // namespace hf

@@ -4,7 +4,8 @@ The kernel (gemm_item_split, grouped_gemm.hip) issues, per wavefront: a
 prologue of the sub-steps q = -Q .. -1 of the steady pattern, then at each
 sub-step j = H*s + half a wait `s_waitcnt vmcnt(split_after(...))`, a barrier,
 A(j + DA) (NAD DMA instructions) and, on half 0, B(s + DB) (NBD), then the
-multiply of A(j) against B(s).  Indices outside the item load a clamped stage
+multiply of A(j) against B(s).  The wide gate/up tiles (grouped_gemm_wide_kernel)
+have a pipeline of their own, checked the same way (simulate_wide).  Indices outside the item load a clamped stage
 into the slot of the unclamped index.  Vector memory loads complete in issue
 order, so the wait is safe when no more than split_after instructions were
 issued after both A(j) and B(s) -- counted here by brute force over whole
@@ -24,13 +25,24 @@ import pytest
 DRIVER_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "split_pipeline")
 
 
-@pytest.fixture(scope="module")
-def configs():
+def driver_lines():
     subprocess.run(["make", "-s", "-C", DRIVER_DIR], check=True)
     out = subprocess.run([os.path.join(DRIVER_DIR, "driver")], capture_output=True, text=True, check=True).stdout
-    rows = [list(map(int, line.split())) for line in out.strip().splitlines()]
+    return out.strip().splitlines()
+
+
+@pytest.fixture(scope="module")
+def configs():
+    rows = [list(map(int, line.split())) for line in driver_lines() if not line.startswith("wide")]
     keys = ["rows", "swiglu", "h", "cb", "da", "db", "nad", "nbd", "after0", "after1", "lds", "a_skip"]
     return [dict(zip(keys, r)) for r in rows]
+
+
+@pytest.fixture(scope="module")
+def wide():
+    line = [ln for ln in driver_lines() if ln.startswith("wide")]
+    assert len(line) == 1
+    return dict(zip(["nad", "nwh", "after0", "after1"], map(int, line[0].split()[1:])))
 
 
 def simulate(c, nk, nad=None):
@@ -119,3 +131,56 @@ def test_a_count_that_is_one_too_large_is_caught(configs):
         except AssertionError:
             broken += 1
     assert broken == len(configs)
+
+
+def simulate_wide(w, H, nk, nad):
+    """The wide gate/up tiles' issue sequence for one item (split_pipeline.h,
+    wide_after): a prologue of A(0) and weight half-stages 0, 1, 2, then per
+    sub-step j = H*s + half a wait, A(j + 1) (nad instructions) and, on a
+    stage's last sub-step, weight half-stages 2s + 3 and 2s + 4.  Every wait
+    must cover the loads the sub-step multiplies; the weight ring slots
+    refilled must not hold a half-stage still to be multiplied."""
+    NWH = w["nwh"]
+    nj = nk * H
+    seq = []
+
+    def issue(kind, i, n):
+        if kind == "A" and i < nj or kind == "W" and i < 2 * nk:
+            seq.append((kind, i, n))
+
+    issue("A", 0, nad)
+    for q in range(3):
+        issue("W", q, NWH)
+    for j in range(nj):
+        s, half = divmod(j, H)
+        need = [("A", j)] + ([("W", 2 * s), ("W", 2 * s + 1)] if half == 0 else [])
+        idx = [next(i for i, (k, x, _) in enumerate(seq) if (k, x) == nd) for nd in need]
+        after = sum(n for (_, _, n) in seq[max(idx) + 1:])
+        steady = s + 1 < nk
+        allowed = (w["after0"] if half == 0 else w["after1"]) if (half == 1 or steady) else 0
+        assert 0 <= allowed <= after, (H, nk, nad, j, allowed, after)
+        issue("A", j + 1, nad)
+        if half == H - 1:
+            # slots of stage s's half-stages get the next ones; the half-stage
+            # in flight (2s + 2) keeps its own
+            assert {(2 * s + 3) % 3, (2 * s + 4) % 3} == {(2 * s) % 3, (2 * s + 1) % 3}
+            issue("W", 2 * s + 3, NWH)
+            issue("W", 2 * s + 4, NWH)
+    assert all(x < (nj if k == "A" else 2 * nk) for k, x, _ in seq)
+
+
+def test_wide_tiles_waits_are_safe(wide):
+    for H in (1, 2):
+        for nk in range(1, 12):
+            for nad in range(wide["nad"] + 1):
+                simulate_wide(wide, H, nk, nad)
+
+
+def test_wide_tiles_one_more_outstanding_is_caught(wide):
+    # The first sub-step of a stage leaves exactly the last half-stage's DMAs
+    # outstanding: one more, and the wait no longer covers half-stage 2s + 1.
+    for H in (1, 2):
+        with pytest.raises(AssertionError):
+            simulate_wide(dict(wide, after0=wide["after0"] + 1), H, 4, wide["nad"])
+    with pytest.raises(AssertionError):
+        simulate_wide(dict(wide, after1=wide["after1"] + 1), 2, 4, 0)
