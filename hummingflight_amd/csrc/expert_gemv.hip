@@ -183,7 +183,9 @@ __global__ __launch_bounds__(256) void gateup_t1_kernel(const float* __restrict_
 // over the slots in a fixed order -- routed slots in rank order, then the
 // shared slices, then `addend` -- the association of glm_forward.cpp:639-640,
 // 658-660 (moeOut += w*y; out = moeOut + sharedOut).
-constexpr int down_batch_rows(int ich) { return 16 / ich > 0 ? 16 / ich : 1; }
+// (one row per batch from 8 chunks on: two rows' weights beside h would take
+// more than the 128 registers a 1024-thread block leaves a lane, and spill)
+constexpr int down_batch_rows(int ich) { return ich >= 8 ? 1 : 16 / ich; }
 
 template <int ICH>
 __global__ __launch_bounds__(1024) void down_t1_kernel(const float* __restrict__ h, LayerDev L,

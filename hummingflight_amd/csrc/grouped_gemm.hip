@@ -1408,7 +1408,12 @@ static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
 template <int EPI>
 static hipError_t launch_epi(const GemmArgs& a, int blocks, hipStream_t s) {
     if (!a.a_lo) return launch_shape<EPI, kLoNone>(a, blocks, s);
-    if (a.a_lo_flag) return launch_shape<EPI, kLoByFlag>(a, blocks, s);
+    if (a.a_lo_flag) {
+        // the flag is x's (gate/up, router, dense layers); the down
+        // projection's h always carries both halves
+        if constexpr (EPI != EPI_SCATTER) return launch_shape<EPI, kLoByFlag>(a, blocks, s);
+        return hipErrorInvalidValue;
+    }
     return launch_shape<EPI, kLoAlways>(a, blocks, s);
 }
 

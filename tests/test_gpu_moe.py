@@ -47,6 +47,21 @@ def test_decode_small_layer(hf, n_group, topk_group):
     r.free()
 
 
+@pytest.mark.parametrize("inter", [3072, 4096])
+def test_decode_wide_intermediate(hf, inter):
+    # Intermediate sizes of 2049-4096 take the decode down kernel's eight
+    # 16-byte chunks per lane, one row per batch; checked end to end against
+    # the oracle, with the shared expert.
+    dims = dict(hidden=1024, inter=inter, n_experts=16, top_k=4)
+    r = Run(dims, n_group=4, topk_group=2, seed=12)
+    x = synth.make_x_dev(1, dims["hidden"], seed=12)
+    res = r.forward(x)
+    xh = x.download(np.float32, dims["hidden"])
+    r.check_token(xh, res, 0)  # selection, weights and output against the oracle
+    x.free()
+    r.free()
+
+
 def test_decode_matches_reference_golden_small(hf, golden):
     cases = [c for c in golden["moe_layer"] if c["name"] == "small"]
     c0 = cases[0]
