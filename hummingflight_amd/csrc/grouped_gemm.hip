@@ -15,7 +15,7 @@
 // The MoE GEMMs stream expert weights (B) far more than they compute: at
 // T = 4096 each expert sees ~128 rows, 128 FLOP per weight byte, below the
 // MI355X ridge (~312), and at T = 64 a few rows.  So the kernels are built to
-// keep B streaming and to spend MFMA cycles only on rows that exist.  Two
+// keep B streaming and to spend MFMA cycles only on rows that exist.  Three
 // tile shapes:
 //   * 128 (M) x 128 (N) x 64 (K), 4 wavefronts (batched decode, router):
 //     wavefront w owns tile rows [32w, 32w + 32) across all 128 columns and
@@ -24,9 +24,13 @@
 //     memory into an LDS ring by DMA (global_load_lds_dwordx4), A fragments
 //     straight into registers (L2-resident activations, row-gathered through
 //     a_rowmap), both 2-4 K stages ahead of the one multiplied;
-//   * 192 (M) x 256 or 384 (N) x 64 (K), 8 wavefronts (prefill): both
-//     operands by DMA into LDS, wavefronts split 2 (row-block parity) x 4
-//     (column groups) -- gemm_item_split below.
+//   * 192 (M) x 256 or 384 (N) x 64 (K), 8 wavefronts (prefill down
+//     projection, dense layers, LM head): both operands by DMA into LDS,
+//     wavefronts split 2 (row-block parity) x 4 (column groups) --
+//     gemm_item_split below;
+//   * 192 (M) x 512 (N) x 64 (K), 8 wavefronts of 64 weight rows each over
+//     all rows (prefill gate/up): weights through private per-wavefront LDS
+//     rings -- gemm_item_wide below.
 // Persistent workgroups walk per-XCD item lists, n fastest, so an M tile's
 // activations are reused within that XCD's L2 (item_range).
 //
