@@ -267,6 +267,35 @@ def test_grouped_edge_shapes(hf, name, dims, routing, n_group, topk_group, n_sha
     r.free()
 
 
+@pytest.mark.parametrize("hidden,inter", [(64, 256), (128, 512)], ids=["one_k_stage", "two_k_stages"])
+@pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
+def test_wide_tiles_few_k_stages(hf, monkeypatch, hidden, inter, fp32_x):
+    # The gate/up GEMM's 512-weight-row tiles with one or two K stages (its
+    # pipeline's tail waits from the first sub-step on), at prefill tile sizes
+    # (400 tokens over 16 experts), with one and two halves of x: every token
+    # against the oracle, and bit for bit against the 256-row tiles.
+    dims = dict(hidden=hidden, inter=inter, n_experts=16, top_k=4)
+    T = 400
+    r = Run(dims, n_group=4, topk_group=2, seed=71, T=T)
+    x = synth.make_x_dev(T, hidden, seed=71)
+    xh = x.download(np.float32, T * hidden).reshape(T, -1)
+    if fp32_x:
+        xh = (xh * (1.0 + np.float32(2.0 ** -10) * np.random.default_rng(71).standard_normal(xh.shape))).astype(
+            np.float32)
+        x.free()
+        x = capi.DeviceBuffer.of(xh)
+    res = r.forward(x, T)
+    check_dispatch(res, dims["n_experts"])
+    for t in range(T):
+        r.check_token(xh[t], res, t)
+    monkeypatch.setenv("HFMOE_PREFILL_WIDE", "0")
+    narrow = r.forward(x, T)
+    monkeypatch.delenv("HFMOE_PREFILL_WIDE")
+    assert np.array_equal(res["out"].view(np.uint32), narrow["out"].view(np.uint32))
+    x.free()
+    r.free()
+
+
 def test_batched_decode_t64_zipf(hf):
     # Batched decode at full shape: 64 tokens, correction bias calibrated for
     # Zipf(1.1) expert popularity (tests/golden/zipf_bias_e256.json), the
