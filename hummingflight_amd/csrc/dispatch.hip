@@ -44,47 +44,58 @@ __device__ __forceinline__ int block_scan(int v, int* wsum) {
     return v + before;
 }
 
-// Offsets, counts and the M-tile list from the per-expert counts cnt[E] (LDS);
-// cursor[e] = offsets[e].  Then the shared group: rows npairs + i <- token i.
-__device__ void dispatch_plan(const int* cnt, int* cursor, int npairs, int E, int tile_rows, int shared_rows,
+// Offsets, counts and the M-tile lists (tl[0], and tl[1] when its rows are
+// set) from the per-expert counts cnt[E] (LDS); cursor[e] = offsets[e].  Then
+// the shared group: rows npairs + i <- token i.
+__device__ void dispatch_plan(const int* cnt, int* cursor, int npairs, int E, const TileList* tl, int shared_rows,
                               int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
-                              int* __restrict__ row_token, int* __restrict__ tile_expert,
-                              int* __restrict__ tile_row0, int* __restrict__ ntiles_out,
-                              unsigned* __restrict__ item_ctr, int* wsum, int* totals) {
+                              int* __restrict__ row_token, unsigned* __restrict__ item_ctr, int* wsum, int* totals) {
     const int t = threadIdx.x;
     if (item_ctr && t < kItemCounters) item_ctr[t] = 0u;  // the grouped GEMMs' work counters
+    const int nl = tl[1].rows > 0 ? 2 : 1;
     // Scans over experts in chunks of 1024 (E <= 1024 in practice: one chunk).
-    int run_rows = 0, run_tiles = 0;
+    int run_rows = 0, run_tiles[2] = {0, 0};
     for (int e0 = 0; e0 < E; e0 += kDispatchThreads) {
         const int e = e0 + t;
         const int c = e < E ? cnt[e] : 0;
-        const int nt = (c + tile_rows - 1) / tile_rows;
         const int c_inc = block_scan(c, wsum);
-        const int t_inc = block_scan(nt, wsum);
+        const int r0 = run_rows + c_inc - c;
         if (e < E) {
-            const int r0 = run_rows + c_inc - c;
-            const int tl0 = run_tiles + t_inc - nt;
             offsets[e] = r0;
             cursor[e] = r0;
             counts[e] = c;
-            for (int j = 0; j < nt; ++j) {
-                tile_expert[tl0 + j] = e;
-                tile_row0[tl0 + j] = r0 + j * tile_rows;
-            }
         }
-        if (t == kDispatchThreads - 1) {
-            totals[0] = c_inc;
-            totals[1] = t_inc;
+        if (t == kDispatchThreads - 1) totals[0] = c_inc;
+#pragma unroll
+        for (int l = 0; l < 2; ++l) {
+            if (l >= nl) break;
+            const int rows = tl[l].rows;
+            const int nt = (c + rows - 1) / rows;
+            const int t_inc = block_scan(nt, wsum);
+            const int tl0 = run_tiles[l] + t_inc - nt;
+            for (int j = 0; j < nt; ++j) {
+                tl[l].expert[tl0 + j] = e;
+                tl[l].row0[tl0 + j] = r0 + j * rows;
+            }
+            if (t == kDispatchThreads - 1) totals[1 + l] = t_inc;
         }
         __syncthreads();
         run_rows += totals[0];
-        run_tiles += totals[1];
+#pragma unroll
+        for (int l = 0; l < 2; ++l)
+            if (l < nl) run_tiles[l] += totals[1 + l];
         __syncthreads();
     }
-    const int shared_tiles = (shared_rows + tile_rows - 1) / tile_rows;
-    for (int j = t; j < shared_tiles; j += kDispatchThreads) {
-        tile_expert[run_tiles + j] = E;
-        tile_row0[run_tiles + j] = npairs + j * tile_rows;
+#pragma unroll
+    for (int l = 0; l < 2; ++l) {
+        if (l >= nl) break;
+        const int rows = tl[l].rows;
+        const int shared_tiles = (shared_rows + rows - 1) / rows;
+        for (int j = t; j < shared_tiles; j += kDispatchThreads) {
+            tl[l].expert[run_tiles[l] + j] = E;
+            tl[l].row0[run_tiles[l] + j] = npairs + j * rows;
+        }
+        if (t == 0) *tl[l].count = run_tiles[l] + shared_tiles;
     }
     for (int i = t; i < shared_rows; i += kDispatchThreads) {
         perm[npairs + i] = npairs + i;
@@ -93,7 +104,6 @@ __device__ void dispatch_plan(const int* cnt, int* cursor, int npairs, int E, in
     if (t == 0) {
         offsets[E] = run_rows;
         offsets[E + 1] = run_rows + shared_rows;
-        *ntiles_out = run_tiles + shared_tiles;
     }
     __syncthreads();
 }
@@ -150,19 +160,18 @@ __device__ void dispatch_count(const int* __restrict__ idx, int begin, int end, 
 
 // Small batches: everything in one workgroup.
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
-    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, int tile_rows, int shared_rows,
-    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
-    int* __restrict__ row_token, int* __restrict__ tile_expert, int* __restrict__ tile_row0,
-    int* __restrict__ ntiles_out, unsigned* __restrict__ item_ctr) {
+    const int* __restrict__ idx, int npairs, int k, int E, int key_bits, TileList tl0, TileList tl1,
+    int shared_rows, int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm,
+    int* __restrict__ row_token, unsigned* __restrict__ item_ctr) {
     extern __shared__ int smem[];
     int* cnt = smem;              // [E]
     int* cursor = cnt + E;        // [E]
     int* whist = cursor + E;      // [waves][E]
     __shared__ int wsum[kDispatchWaves];
-    __shared__ int totals[2];
+    __shared__ int totals[3];
+    const TileList tl[2] = {tl0, tl1};
     dispatch_count(idx, 0, npairs, E, cnt);
-    dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
-                  tile_row0, ntiles_out, item_ctr, wsum, totals);
+    dispatch_plan(cnt, cursor, npairs, E, tl, shared_rows, counts, offsets, perm, row_token, item_ctr, wsum, totals);
     dispatch_scatter(idx, 0, npairs, k, E, key_bits, cursor, whist, perm, row_token);
 }
 
@@ -180,15 +189,15 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(const 
 // Step 2: one workgroup sums the chunk counts, plans offsets and tiles, and
 // turns chunk_hist[b][e] into the first slot of chunk b's expert-e pairs.
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
-    int nchunks, int npairs, int E, int tile_rows, int shared_rows, int* __restrict__ chunk_hist,
+    int nchunks, int npairs, int E, TileList tl0, TileList tl1, int shared_rows, int* __restrict__ chunk_hist,
     int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ perm, int* __restrict__ row_token,
-    int* __restrict__ tile_expert, int* __restrict__ tile_row0, int* __restrict__ ntiles_out,
     unsigned* __restrict__ item_ctr) {
     extern __shared__ int smem[];
     int* cnt = smem;        // [E]
     int* cursor = cnt + E;  // [E]
     __shared__ int wsum[kDispatchWaves];
-    __shared__ int totals[2];
+    __shared__ int totals[3];
+    const TileList tl[2] = {tl0, tl1};
     for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
         int c = 0;
 #pragma unroll 8
@@ -196,8 +205,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_plan_kernel(
         cnt[e] = c;
     }
     __syncthreads();
-    dispatch_plan(cnt, cursor, npairs, E, tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert,
-                  tile_row0, ntiles_out, item_ctr, wsum, totals);
+    dispatch_plan(cnt, cursor, npairs, E, tl, shared_rows, counts, offsets, perm, row_token, item_ctr, wsum, totals);
     for (int e = threadIdx.x; e < E; e += kDispatchThreads) {
         int run = cursor[e];
 #pragma unroll 8
@@ -229,9 +237,10 @@ static hipError_t raise_lds(const void* fn, size_t lds, size_t& raised) {
     return e;
 }
 
-hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
-                           int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, int* chunk_hist, unsigned* item_ctr, hipStream_t s) {
+hipError_t launch_dispatch(const int* idx, int T, int k, int E, const TileList& tl0, const TileList& tl1,
+                           int shared_rows, int* counts, int* offsets, int* perm, int* row_token, int* chunk_hist,
+                           unsigned* item_ctr, hipStream_t s) {
+    if (tl0.rows <= 0 || tl1.rows < 0) return hipErrorInvalidValue;
     int bits = 1;
     while ((1 << bits) < E) ++bits;
     const int npairs = T * k;
@@ -242,8 +251,7 @@ hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, i
         hipError_t e = raise_lds(reinterpret_cast<const void*>(dispatch_kernel), lds, raised);
         if (e != hipSuccess) return e;
         return launch(dispatch_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds, s, idx, npairs, k, E, bits,
-                      tile_rows, shared_rows, counts, offsets, perm, row_token, tile_expert, tile_row0, ntiles,
-                      item_ctr);
+                      tl0, tl1, shared_rows, counts, offsets, perm, row_token, item_ctr);
     }
     // One chunk of whole passes per workgroup, at most kDispatchMaxChunks chunks.
     const int per = (passes + kDispatchMaxChunks - 1) / kDispatchMaxChunks;
@@ -261,8 +269,7 @@ hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, i
                    chunk, chunk_hist);
     if (e == hipSuccess)
         e = launch(dispatch_plan_kernel, dim3(1), dim3(kDispatchThreads), (uint32_t)lds_plan, s, nchunks, npairs, E,
-                   tile_rows, shared_rows, chunk_hist, counts, offsets, perm, row_token, tile_expert, tile_row0,
-                   ntiles, item_ctr);
+                   tl0, tl1, shared_rows, chunk_hist, counts, offsets, perm, row_token, item_ctr);
     if (e == hipSuccess)
         e = launch(dispatch_scatter_kernel, dim3(nchunks), dim3(kDispatchThreads), (uint32_t)lds_scatter, s, idx,
                    npairs, k, E, bits, chunk, static_cast<const int*>(chunk_hist), perm, row_token);

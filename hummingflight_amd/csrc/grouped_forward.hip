@@ -52,7 +52,7 @@ static int expert_tile_rows(int T) {
 void grouped_workspace_free() {
     GroupedWorkspace& w = g.gws;
     void* ptrs[] = {w.counts, w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0, w.ntiles,
-                    w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
+                    w.tile_expert_gu, w.tile_row0_gu, w.chunk_hist, w.item_ctr, w.lo_flag, w.xh, w.xl, w.hh, w.hl, w.y, w.part};
     for (void* p : ptrs)
         if (p) hipFree(p);
     w = GroupedWorkspace{};
@@ -81,6 +81,8 @@ int grouped_workspace_alloc() {
         {(void**)&w.tile_expert, sizeof(int) * w.max_tiles},
         {(void**)&w.tile_row0, sizeof(int) * w.max_tiles},
         {(void**)&w.ntiles, 256},
+        {(void**)&w.tile_expert_gu, sizeof(int) * w.max_tiles},
+        {(void**)&w.tile_row0_gu, sizeof(int) * w.max_tiles},
         {(void**)&w.chunk_hist, sizeof(int) * (size_t)kDispatchMaxChunks * c.E},
         {(void**)&w.item_ctr, sizeof(unsigned) * kItemCounters},
         {(void**)&w.lo_flag, 256},
@@ -112,10 +114,14 @@ int grouped_workspace_alloc() {
 int grouped_tile_rows(int T) { return expert_tile_rows(T); }
 
 // The prefill gate/up GEMM takes the wide tiles (512 weight rows, 256
-// outputs of h) unless HFMOE_PREFILL_WIDE=0 (256 weight rows): the down
-// projection keeps its 384-row tiles, on which its two halves of h cost fewer
-// LDS reads per weight byte.
-static bool prefill_wide() { return env_int("HFMOE_PREFILL_WIDE", 1) != 0; }
+// outputs of h; 192 rows, or 160 from a second tile list when x has a lo
+// half) when the intermediate size is a multiple of 256, unless
+// HFMOE_PREFILL_WIDE=0 (192 x 256 tiles): the down projection keeps its 192 x
+// 384 tiles, on which its two halves of h cost fewer LDS reads per weight
+// byte.
+static bool prefill_wide(int TR) {
+    return TR == kPrefillTileRows && g.cfg.I % (kWideTileCols / 2) == 0 && env_int("HFMOE_PREFILL_WIDE", 1) != 0;
+}
 
 int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     const Cfg& c = g.cfg;
@@ -151,9 +157,10 @@ int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     prof_begin(p, "select", s);
     HF_CHECK_LAUNCH(launch_select(g.ws.scores, T, c, g.ws.idx, g.ws.wts, s), "select");
     prof_begin(p, "dispatch", s);
-    HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, TR, shared_rows, w.counts,
-                                    w.offsets, w.perm, w.row_token, w.tile_expert, w.tile_row0,
-                                    w.ntiles, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
+    TileList tl{TR, w.tile_expert, w.tile_row0, w.ntiles}, tl_gu{};
+    if (prefill_wide(TR)) tl_gu = TileList{kWideTileRows, w.tile_expert_gu, w.tile_row0_gu, w.ntiles + 32};
+    HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, tl, tl_gu, shared_rows, w.counts, w.offsets, w.perm,
+                                    w.row_token, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
                     "dispatch");
     return HFMOE_OK;
 }
@@ -168,15 +175,22 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
 
     // Gate/up of every group: the routed experts' (token, rank) rows and the
     // shared expert's token rows (group E), one launch.
+    const bool wide = prefill_wide(TR);
     GemmArgs gu{};
     gu.K = c.d;
     gu.N = c.I;
     gu.tile_rows = TR;
-    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU, c.I, prefill_wide());
+    gu.tile_cols = gemm_tile_cols(TR, EPI_SWIGLU, c.I, wide);
     gu.n_tiles = gemm_n_tiles(EPI_SWIGLU, c.I, gu.tile_cols);
     gu.tile_group = w.tile_expert;
     gu.tile_row0 = w.tile_row0;
     gu.ntiles_dev = w.ntiles;
+    if (wide) {  // x with a lo half: the 160-row tiles
+        gu.lo_tiles.group = w.tile_expert_gu;
+        gu.lo_tiles.row0 = w.tile_row0_gu;
+        gu.lo_tiles.count = w.ntiles + 32;
+        gu.lo_tiles.shared_mtiles = (shared_rows + kWideTileRows - 1) / kWideTileRows;
+    }
     gu.group_end = w.offsets + 1;
     gu.rows_total = P + shared_rows;
     gu.a_hi = w.xh;

@@ -28,9 +28,10 @@
 //     projection, dense layers, LM head): both operands by DMA into LDS,
 //     wavefronts split 2 (row-block parity) x 4 (column groups) --
 //     gemm_item_split below;
-//   * 192 (M) x 512 (N) x 64 (K), 8 wavefronts of 64 weight rows each over
-//     all rows (prefill gate/up): weights through private per-wavefront LDS
-//     rings -- gemm_item_wide below.
+//   * 192 or 160 (M) x 512 (N) x 64 (K), 8 wavefronts of 64 weight rows each
+//     over all rows (prefill gate/up; 160-row tiles when x has a lo half):
+//     weights through private per-wavefront LDS rings -- gemm_item_wide
+//     below.
 // Persistent workgroups walk per-XCD item lists, n fastest, so an M tile's
 // activations are reused within that XCD's L2 (item_range).
 //
@@ -94,6 +95,12 @@ __device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* l) {
 // for every LDS read with lgkmcnt(0)), a buffer DMA leaves the compiler free
 // to wait for just the read it needs, so LDS reads can run ahead of the
 // multiplies that use them.
+// c ? x : y on values: a conditional on two named resources can compile to a
+// select of their addresses, which keeps them in scratch memory.
+template <class T>
+__device__ __forceinline__ T pick(bool c, T x, T y) {
+    return c ? x : y;
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
     // stride 0, 4 GiB of records, 32-bit data format (untyped loads)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
@@ -947,7 +954,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
 
 // ---------------------------------------------------------------------------
 // Wide prefill gate/up tiles: 192 (M) x 512 (N: 256 gate + 256 up weight
-// rows) x 64 (K), eight wavefronts, one workgroup per CU.
+// rows) x 64 (K), or 160 x 512 x 64 when x has a lo half, eight wavefronts,
+// one workgroup per CU.
 //
 // What bounds the prefill gate/up GEMM is the CU's stream of line requests to
 // L2: the weights once, plus the activation rows once per N tile.  Per weight
@@ -955,24 +963,28 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
 // of 256 cut that from 0.56 to 0.28 (BF16-valued x) and from 1.12 to 0.56
 // (FP32 x: hi and lo halves).  Registers and LDS set the layout:
 //   * wavefront w owns weight rows [64 w, 64 w + 64) of the tile (32 gate
-//     rows then the 32 matching up rows) and all 192 rows of the M tile:
+//     rows then the 32 matching up rows) and all rows of the M tile: up to
 //     12 x 4 accumulator blocks, 192 of its 256 registers, and no weight
 //     fragment is read by two wavefronts;
 //   * so each wavefront streams its own weights, in 128-byte lines, through a
-//     private LDS ring of three half-stages (32 rows x 64 k, 4 KB), reading a
-//     k half's weight fragments into registers before multiplying with them;
-//     a stage's last sub-step refills the two slots it read with the next
-//     half-stages as soon as its first k half is done, so 1.5 stages of
-//     weights stay in flight per wavefront with no barrier among wavefronts
-//     for them;
+//     private LDS ring of three half-stages (32 rows x 64 k, 4 KB), reading
+//     a stage's weight fragments into registers before multiplying with them
+//     (with two halves of A, all 32 registers of them once per stage, kept
+//     for the second half: room that the 160-row tiles' 160 accumulator
+//     registers leave, and the reason for those tiles); the slots read are
+//     refilled with the next half-stages as soon as their reads have landed,
+//     so 1.5 stages of weights stay in flight per wavefront with no barrier
+//     among wavefronts for them;
 //   * the activations (shared by all eight wavefronts) go by DMA into a
-//     two-slot ring of sub-steps (192 rows x 64 k; a K stage has one sub-step
-//     per half of A), with one barrier per sub-step.
+//     two-slot ring of sub-steps (up to 192 rows x 64 k; a K stage has one
+//     sub-step per half of A), with one barrier per sub-step.
 // 2 x 24 KB of activations + 8 x 3 x 4 KB of weights = 144 KB of LDS.
-// The cost of this layout is LDS reads: every wavefront reads all rows'
-// activation fragments, and with two halves of A its weight fragments twice
-// per stage (no registers are left to keep them), 6.5 bytes per weight byte
-// against 5 for the down projection's 384-row tiles, which therefore stay.
+// With one half of A the 192-row tiles measure faster (fewer shared-expert
+// tiles); the 160-row ones still hold a near-uniform prefill's ~128-row
+// experts in one tile.  The cost of this layout is LDS reads: every
+// wavefront reads all rows' activation fragments; the down projection's two
+// halves of h would cost more LDS reads per weight byte here than on its
+// 384-row tiles, which therefore stay.
 constexpr int kWideWaves = 8;
 constexpr int kWideWaveRows = kWideTileCols / kWideWaves;  // weight rows per wavefront
 constexpr int kWideHalfRows = kWideWaveRows / 2;           // weight rows per half-stage
@@ -981,21 +993,24 @@ constexpr size_t kWideLds = 2 * (2 * (size_t)kPrefillTileRows * GBK +
                                  (size_t)kWideWaves * kWideWRing * kWideHalfRows * GBK);
 static_assert(kWideLds + 64 <= 160 * 1024, "wide LDS");
 
-// Sub-step j = H * s + half multiplies A half `half` of K stage s.  Issue
-// order: sub-step j issues A(j + 1) over its first k half (after its
-// barrier); the last sub-step of stage s issues weight half-stages 2s + 3 and
-// 2s + 4 over its second k half (into the two ring slots stage s came from,
-// whose reads have all landed by then).  Loads complete in issue order, so
-// the first sub-step of stage s, which needs A(j) and weight half-stages 2s
-// and 2s + 1, may leave exactly half-stage 2s + 2 (one half-stage's DMAs)
-// outstanding, and a second sub-step nothing.
+// Sub-step j = H * s + half multiplies A half `half` of K stage s.  The
+// first sub-step of a stage reads the wavefront's weight fragments of stage s
+// (half-stages 2s, 2s + 1) from its ring; with two halves it reads them all
+// at once and keeps them in registers for the second.  Issue order: sub-step
+// j issues A(j + 1) over its first k half (after its barrier) and weight
+// half-stages over its second k half, into the ring slots stage s came from
+// (whose reads have all landed by then): 2s + 3 and 2s + 4 with one half,
+// else 2s + 3 from the first sub-step and 2s + 4 from the second.  Loads
+// complete in issue order, so a sub-step may leave exactly the last weight
+// half-stage issued before it outstanding (split_pipeline.h: wide_after).
 template <int HALVES, class Setup>
 __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
                                                Setup&& on_setup) {
-    constexpr int ROWS = kPrefillTileRows;
+    constexpr int ROWS = HALVES == 1 ? kPrefillTileRows : kWideTileRows;
     constexpr int AST = ROWS * GBK;                 // elements per A sub-step slot
-    constexpr int NAD = ROWS / 8 / kWideWaves;      // A DMAs (8 rows x 128 bytes) per wavefront per sub-step
+    constexpr int NAD = (ROWS / 8 + kWideWaves - 1) / kWideWaves;  // A DMAs (8 rows x 128 bytes) per wavefront
     constexpr int NWH = kWideHalfRows / 8;          // weight DMAs per half-stage
+    constexpr int NWS = wide_w_per_substep(HALVES);  // weight half-stages issued per sub-step
     static_assert(NAD == 3 && NWH == 4, "the counts tests/split_pipeline checks the waits with");
     constexpr int WHS = kWideHalfRows * GBK;        // elements per weight half-stage slot
     constexpr int CB = kWideWaveRows / 16;          // column blocks per wavefront
@@ -1026,7 +1041,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     // reads (16 rows x 16 bytes per quarter wavefront).
     const int dr = lane >> 3;
     const int dc = (lane & 7) ^ dr;
-    // A: 8-row block 4 i + wave of the tile (rows past the item's last re-read
+    // A: 8-row block 8 i + wave of the tile (rows past the item's last re-read
     // it; blocks past its last 16-row block are not loaded at all).
     uint32_t aoff[NAD];
 #pragma unroll
@@ -1050,8 +1065,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     auto issue_a1 = [&](int j, int i, int nab) {
         const int blk = kWideWaves * i + wave;
         if (j >= nj || blk >= nab) return;
-        const __amdgpu_buffer_rsrc_t ra = (j % HALVES) ? ra1 : ra0;
-        dma16<0>(ra, aoff[i], (uint32_t)(j / HALVES) * (2 * GBK), aring + (j & 1) * AST + blk * 512);
+        dma16<0>(pick((j % HALVES) != 0, ra1, ra0), aoff[i], (uint32_t)(j / HALVES) * (2 * GBK), aring + (j & 1) * AST + blk * 512);
     };
     auto issue_a = [&](int j, int nab) {
 #pragma unroll
@@ -1061,7 +1075,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     auto issue_w1 = [&](int q, int i) {
         if (q >= 2 * nk) return;
         const int s = q >> 1, h = q & 1;
-        dma16(h ? rw1 : rw0, woff, (uint32_t)s * (2 * GBK) + (uint32_t)(8 * i) * wrow_bytes,
+        dma16(pick(h != 0, rw1, rw0), woff, (uint32_t)s * (2 * GBK) + (uint32_t)(8 * i) * wrow_bytes,
               wring + (q % kWideWRing) * WHS + i * 512);
     };
     auto issue_w = [&](int q) {
@@ -1080,7 +1094,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     issue_w(1);
     issue_w(2);
 
-    // The K loop, compiled per row-block count of the item (all four
+    // The K loop, compiled per row-block count of the item (all eight
     // wavefronts share it), so every sub-step's multiplies are straight code.
     auto kloop = [&](auto nm_c) __attribute__((always_inline)) {
         constexpr int NM = decltype(nm_c)::value;
@@ -1089,17 +1103,20 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
         for (int j = 0; j < NM; ++j)
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) acc[j][cb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        u32x4 wk[2][CB];  // the stage's weight fragments [k half][column block]
         // One sub-step's multiplies: per k half, the CB weight fragments of
-        // that half (read from the wavefront's ring; the second half's reads
-        // go out one by one as the first half's last multiplies free their
-        // registers), each activation fragment (read one step ahead) against
+        // that half, each activation fragment (read one step ahead) against
+        // them.  The weight fragments come from the wavefront's ring: with one
+        // half of A, the second k half's reads go out one by one as the first
+        // half's last multiplies free their registers; with two, a stage's
+        // first sub-step reads all of them up front and the second reuses
         // them.  The DMAs go out one at a time between row blocks rather than
         // in a burst (a DMA waits at issue while the CU's queue of line
         // requests is full, holding up the multiplies behind it): A(j + 1)
-        // over the first k half; in a stage's last sub-step (LAST), weight
-        // half-stages 2s + 3 and 2s + 4 over the second, once every read of
-        // the ring slots they overwrite has landed.
-        auto compute = [&](const uint16_t* at, int s, bool last, int jn, int nab) __attribute__((always_inline)) {
+        // over the first k half; the weight half-stages from wq on over the
+        // second, once every read of the ring slots they overwrite has landed.
+        auto compute = [&](const uint16_t* at, int s, bool first, int jn, int nab, int wq)
+                           __attribute__((always_inline)) {
             const uint16_t* w0 = wring + ((2 * s) % kWideWRing) * WHS;
             const uint16_t* w1 = wring + ((2 * s + 1) % kWideWRing) * WHS;
             auto wfrag = [&](int cb, int kh) {
@@ -1113,25 +1130,32 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
             // After row block r of k half kh (r == -1: before any).
             auto dmas_after = [&](int kh, int r) {
                 constexpr int NMX = NM > 0 ? NM : 1;
+                constexpr int NW = NWS * NWH;
                 if (kh == 0) {  // A(jn): DMA r + 1 after row block r, the rest after the last
 #pragma unroll
                     for (int i = 0; i < NAD; ++i)
                         if (i == r + 1 || (r == NMX - 1 && i > r + 1)) dma([&] { issue_a1(jn, i, nab); });
-                } else if (last) {  // 2 NWH weight DMAs spread over the row blocks
+                } else {  // NW weight DMAs spread over the row blocks
                     if (r == -1) {
                         asm volatile("" ::: "memory");
                         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slots' reads are done
                     }
 #pragma unroll
-                    for (int k = 0; k < 2 * NWH; ++k)
-                        if (k * NMX / (2 * NWH) == r + 1 || (r == NMX - 1 && k * NMX / (2 * NWH) > r))
-                            dma([&] { issue_w1(2 * s + 3 + k / NWH, k % NWH); });
+                    for (int k = 0; k < NW; ++k)
+                        if (k * NMX / NW == r + 1 || (r == NMX - 1 && k * NMX / NW > r))
+                            dma([&] { issue_w1(wq + k / NWH, k % NWH); });
                 }
             };
             if constexpr (NM > 0) {
-                u32x4 wk[2][CB];  // [k half][column block]
+                if constexpr (HALVES == 1) {
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) wk[0][cb] = wfrag(cb, 0);
+                    for (int cb = 0; cb < CB; ++cb) wk[0][cb] = wfrag(cb, 0);
+                } else if (first) {
+#pragma unroll
+                    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) wk[kh][cb] = wfrag(cb, kh);
+                }
                 u32x4 av[2][NM];
                 av[0][0] = frag(at, fr, fq);
 #pragma unroll
@@ -1147,7 +1171,7 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
                         for (int cb = 0; cb < CB; ++cb) {
                             acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                 as_bf16x8(wk[kh][cb]), as_bf16x8(av[kh][j]), acc[j][cb], 0, 0, 0);
-                            if (kh == 0 && j == NM - 1) wk[1][cb] = wfrag(cb, 1);
+                            if (HALVES == 1 && kh == 0 && j == NM - 1) wk[1][cb] = wfrag(cb, 1);
                         }
                         dmas_after(kh, j);
                         // Keep the reads one step ahead: hoisted further, they
@@ -1157,28 +1181,25 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
                 }
             } else {
                 issue_a(jn, nab);
-                if (last) {
-                    issue_w(2 * s + 3);
-                    issue_w(2 * s + 4);
-                }
+#pragma unroll
+                for (int k = 0; k < NWS; ++k) issue_w(wq + k);
             }
         };
         for (int j = 0; j < nj; ++j) {
             // Sub-step j: A(j); the first of a stage also weight half-stages
-            // 2s, 2s+1 (a second one waits for everything).
+            // 2s, 2s+1.
             const int s = j / HALVES;
             const bool first = HALVES == 1 || (j & 1) == 0;
             // (two ways, as here: a three-way branch around the waits made the
             // compiler schedule the two-half K loop ~35 % slower)
-            static_assert(wide_after(1, NWH) == 0, "a second sub-step waits for everything");
-            if (first && wide_steady(s, nk))
-                wait_vmcnt<wide_after(0, NWH)>();
+            if (wide_steady(s, nk))
+                wait_vmcnt<wide_after(NWH)>();
             else
                 wait_vmcnt<0>();
             lds_barrier();
             int nab = nab0;
             asm volatile("" : "+s"(nab));
-            compute(aring + (j & 1) * AST, s, HALVES == 1 || !first, j + 1, nab);
+            compute(aring + (j & 1) * AST, s, first, j + 1, nab, 2 * s + 3 + (first ? 0 : 1));
         }
         // Every load of the item has landed (the last stage waits for all).
         // h columns n0 + 32 w + 16 cb + 4 fq + q from gate block cb and up block cb + 2.
@@ -1189,8 +1210,8 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
             if (rl < rows) store_tile_row<EPI_SWIGLU, CB>(a, acc[j], row0 + rl, col0, 0, row0 + rl);
         }
     };
-    // Row-block counts in buckets (8 .. 12 exact, the near-uniform prefill's
-    // range; smaller ones rounded up to even): the extra blocks multiply rows
+    // Row-block counts in buckets (8 .. 12 or 10 exact, the near-uniform
+    // prefill's range; smaller ones rounded up to even): the extra blocks multiply rows
     // that were not loaded and are never stored.
     const int nb = nrb >= 8 ? nrb : (nrb + 1) & ~1;
     static_for_desc<ROWS / 16>([&](auto n_c) {
@@ -1202,32 +1223,44 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
 }
 
 // x (BF16 hi, and lo when the device flag says x is not BF16-valued) times
-// the gate and up weights, h = silu(g) * u out as BF16 hi / lo.
+// the gate and up weights, h = silu(g) * u out as BF16 hi / lo.  With the lo
+// half the items are those of the 160-row M tiles (GemmArgs::lo_tiles),
+// else of the 192-row ones.
 __global__ __launch_bounds__(64 * kWideWaves, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t wlds[];  // kWideLds bytes
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int m_tiles = a.ntiles_dev ? *a.ntiles_dev : a.m_tiles;
-    const ItemRange r = item_range<true>(a, m_tiles);
-    const bool use_lo = *a.a_lo_flag != 0u;
     // One item, then a barrier: every wavefront is done with the activation
     // ring before the next item's loads land in it.
-    auto run = [&](int item, auto&& on_setup) __attribute__((always_inline)) {
-        if (group_absent(a, a.tile_group ? a.tile_group[item / a.n_tiles] : 0)) {
-            on_setup();
+    auto items = [&](const GemmArgs& b, auto halves_c) __attribute__((always_inline)) {
+        constexpr int HALVES = decltype(halves_c)::value;
+        const int m_tiles = b.ntiles_dev ? *b.ntiles_dev : b.m_tiles;
+        const ItemRange r = item_range<true>(b, m_tiles);
+        auto run = [&](int item, auto&& on_setup) __attribute__((always_inline)) {
+            if (group_absent(b, b.tile_group ? b.tile_group[item / b.n_tiles] : 0)) {
+                on_setup();
+                return;
+            }
+            gemm_item_wide<HALVES>(b, item, wlds, t, wave, on_setup);
+            lds_barrier();
+        };
+        if (!b.item_ctr || !r.by_mtile) {
+            for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li), [] {});
             return;
         }
-        if (use_lo)
-            gemm_item_wide<2>(a, item, wlds, t, wave, on_setup);
-        else
-            gemm_item_wide<1>(a, item, wlds, t, wave, on_setup);
-        lds_barrier();
+        dynamic_items(b, r, run);
     };
-    if (!a.item_ctr || !r.by_mtile) {
-        for (int li = r.begin; li < r.end; li += r.stride) run(r.item(li), [] {});
-        return;
+    if (*a.a_lo_flag != 0u) {
+        GemmArgs b = a;
+        b.tile_rows = kWideTileRows;
+        b.tile_group = a.lo_tiles.group;
+        b.tile_row0 = a.lo_tiles.row0;
+        b.ntiles_dev = a.lo_tiles.count;
+        b.shared_mtiles = a.lo_tiles.shared_mtiles;
+        items(b, std::integral_constant<int, 2>{});
+    } else {
+        items(a, std::integral_constant<int, 1>{});
     }
-    dynamic_items(a, r, run);
 }
 
 // out[t] = (sum_r w[t, r] * y[t*k + r]) + y[shared_row0 + t] (when shared_row0 >= 0):
@@ -1396,10 +1429,11 @@ template <int EPI, int LOM>
 static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
     if (a.tile_rows == kPrefillTileRows && a.tile_cols == kWideTileCols) {
         // The MoE gate/up GEMM only (on x, whose lo half goes by the device
-        // flag), whole wide tiles (their weight DMAs are not clamped at N),
-        // one K split.
+        // flag, and with the 160-row tile list for it), whole wide tiles
+        // (their weight DMAs are not clamped at N), one K split.
         if constexpr (EPI == EPI_SWIGLU && LOM == kLoByFlag) {
-            if (a.N % (kWideTileCols / 2) == 0 && a.ksplit == 1 && a.a_lo_flag) return launch_gemm_wide(a, blocks, s);
+            if (a.N % (kWideTileCols / 2) == 0 && a.ksplit == 1 && a.a_lo_flag && a.lo_tiles.count)
+                return launch_gemm_wide(a, blocks, s);
         }
         return hipErrorInvalidValue;
     }

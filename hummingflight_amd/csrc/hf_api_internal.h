@@ -36,9 +36,11 @@ struct GroupedWorkspace {
     int* offsets = nullptr;      // [E + 2] group row offsets (group E = shared expert)
     int* perm = nullptr;         // [rows] pair id (y row) of each sorted row
     int* row_token = nullptr;    // [rows] token of each sorted row
-    int* tile_expert = nullptr;  // [max_tiles] group of each 128-row M tile
+    int* tile_expert = nullptr;  // [max_tiles] group of each M tile
     int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
-    int* ntiles = nullptr;       // [1] M tiles in use
+    int* ntiles = nullptr;       // [64] M tiles in use: [0] this list, [32] the wide gate/up list
+    int* tile_expert_gu = nullptr;  // [max_tiles] the wide gate/up tiles (kWideTileRows rows)
+    int* tile_row0_gu = nullptr;
     int* chunk_hist = nullptr;   // [kDispatchMaxChunks, E] dispatch chunk counts / first slots
     unsigned* item_ctr = nullptr;  // [kItemCounters] prefill GEMM work counters (zeroed by the dispatch)
     unsigned int* lo_flag = nullptr;  // [0] x has a nonzero BF16 lo half

@@ -14,8 +14,9 @@ constexpr int kGemmTileK = 64;      // K per pipeline stage (K % (64 * ksplit) =
 enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 
 // Weight rows per tile of the wide prefill gate/up kernel (eight wavefronts
-// of 64 weight rows, 32 gate + 32 up, each over all 192 rows of an M tile).
-constexpr int kWideTileCols = 512;
+// of 64 weight rows, 32 gate + 32 up, each over all rows of an M tile), and
+// the rows of its M tiles when x has a lo half (GemmArgs::lo_tiles).
+constexpr int kWideTileCols = 512, kWideTileRows = 160;
 
 // Weight rows per tile for M tiles of tile_rows rows (MoE prefill: gate/up
 // 512 with wide = true when the N outputs of h divide into whole wide tiles,
@@ -80,6 +81,15 @@ struct GemmArgs {
     // so that its workgroups stream each shared weight tile together through
     // the XCD's L2 rather than once per M tile.  0: no such group.
     int shared_mtiles;
+    // Wide gate/up tiles (tile_cols kWideTileCols): the M tiles the kernel
+    // takes instead when the a_lo_flag is set, kWideTileRows rows each (same
+    // groups; shared_mtiles of them the shared expert's).
+    struct {
+        const int* group;
+        const int* row0;
+        const int* count;
+        int shared_mtiles;
+    } lo_tiles;
 };
 
 // Groups whose b_tab entry (3g + b_which) is null are skipped.
@@ -106,8 +116,19 @@ hipError_t launch_router_reduce(const float* part, int ksplit, int T, int E, con
 // grouped GEMMs that follow it.
 constexpr int kDispatchMaxChunks = 64;
 constexpr int kItemCounters = 16;
-hipError_t launch_dispatch(const int* idx, int T, int k, int E, int tile_rows, int shared_rows,
-                           int* counts, int* offsets, int* perm, int* row_token, int* tile_expert,
-                           int* tile_row0, int* ntiles, int* chunk_hist, unsigned* item_ctr, hipStream_t s);
+// An M-tile list: tile i covers sorted rows [row0[i], +rows) of group
+// expert[i] (clipped to the group's end); count[0] tiles in use.
+struct TileList {
+    int rows = 0;  // rows per tile (0: no list)
+    int* expert = nullptr;
+    int* row0 = nullptr;
+    int* count = nullptr;
+};
+// tl0: the M tiles of both grouped GEMMs; tl1 (when tl1.rows > 0): a second
+// list of the same groups, the wide gate/up kernel's tiles when x has a lo
+// half (GemmArgs::lo_tiles).
+hipError_t launch_dispatch(const int* idx, int T, int k, int E, const TileList& tl0, const TileList& tl1,
+                           int shared_rows, int* counts, int* offsets, int* perm, int* row_token, int* chunk_hist,
+                           unsigned* item_ctr, hipStream_t s);
 
 }  // namespace hf

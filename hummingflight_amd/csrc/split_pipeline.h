@@ -60,14 +60,18 @@ constexpr bool split_a_may_skip(int H, int DA, int DB, int NAD, int NBD) {
 // Wide gate/up tiles (grouped_gemm_wide_kernel): per wavefront, a prologue
 // issues A(0) and weight half-stages 0, 1, 2; sub-step j = H*s + half waits,
 // meets the workgroup at a barrier, issues A(j + 1) (0 .. NAD DMA
-// instructions: the item's used rows) and, on a stage's last sub-step, weight
-// half-stages 2s + 3 and 2s + 4 (NWH each); loads past the item issue
-// nothing.  The first sub-step of stage s needs A(j) and half-stages 2s and
-// 2s + 1, a second sub-step A(j).  Steady count of DMA instructions a
-// sub-step may leave outstanding:
-constexpr int wide_after(int half, int nwh) { return half == 0 ? nwh : 0; }
-// ... valid while the loads it assumes were issued (half-stage 2s + 2
-// exists); otherwise the sub-step waits for everything.
+// instructions: the item's used rows) and weight half-stages
+// 2s + 3 + half, ... (wide_w_per_substep(H) of them, NWH DMAs each: both on a
+// one-half stage, one per sub-step of a two-half stage); loads past the item
+// issue nothing.  The first sub-step of stage s needs A(j) and half-stages 2s
+// and 2s + 1, whose fragments it keeps in registers for a second sub-step,
+// which needs A(j) only.  Steady count of DMA instructions a sub-step may
+// leave outstanding (the last weight half-stage issued before it):
+constexpr int wide_after(int nwh) { return nwh; }
+constexpr int wide_w_per_substep(int halves) { return 2 / halves; }
+// ... valid while the loads it assumes were issued (half-stage 2s + 2, or
+// 2s + 3 for a second sub-step, exists); otherwise the sub-step waits for
+// everything.
 constexpr bool wide_steady(int s, int nk) { return s + 1 < nk; }
 
 }  // namespace hf

@@ -1,7 +1,7 @@
 // Prints the prefill GEMM pipeline parameters (split_pipeline.h) for every
 // configuration the library instantiates: rows swiglu halves cb da db nad nbd
 // after_half0 after_half1 lds_bytes a_may_skip; then the wide gate/up tiles'
-// line: "wide" nad nwh after_half0 after_half1.
+// line: "wide" nad nwh after w_per_substep(1) w_per_substep(2).
 #include <cstdio>
 
 #include "split_pipeline.h"
@@ -19,7 +19,9 @@ int main() {
                             split_after(h, da, db, 0, nad, nbd), h == 2 ? split_after(h, da, db, 1, nad, nbd) : -1,
                             split_lds_max(rows, cb), split_a_may_skip(h, da, db, nad, nbd) ? 1 : 0);
             }
-    // wide gate/up tiles: "wide nad nwh after_half0 after_half1"
-    std::printf("wide %d %d %d %d\n", 192 / 8 / 8, 32 / 8, wide_after(0, 32 / 8), wide_after(1, 32 / 8));
+    // wide gate/up tiles (160-row M tiles, 32-row weight half-stages):
+    // "wide nad nwh after w_per_substep(1) w_per_substep(2)"
+    std::printf("wide %d %d %d %d %d\n", (160 / 8 + 7) / 8, 32 / 8, wide_after(32 / 8), wide_w_per_substep(1),
+                wide_w_per_substep(2));
     return 0;
 }

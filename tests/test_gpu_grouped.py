@@ -271,9 +271,11 @@ def test_grouped_edge_shapes(hf, name, dims, routing, n_group, topk_group, n_sha
 @pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
 def test_wide_tiles_few_k_stages(hf, monkeypatch, hidden, inter, fp32_x):
     # The gate/up GEMM's 512-weight-row tiles with one or two K stages (its
-    # pipeline's tail waits from the first sub-step on), at prefill tile sizes
-    # (400 tokens over 16 experts), with one and two halves of x: every token
-    # against the oracle, and bit for bit against the 256-row tiles.
+    # pipeline's tail waits from the first sub-step on), at prefill tile
+    # sizes (400 tokens over 16 experts: ~100 rows per expert), with one half
+    # of x (192-row tiles) and two (160-row tiles: some experts over 160
+    # rows, and 160 + 160 + 80 shared rows): every token against the oracle,
+    # and bit for bit against the 192 x 256 tiles.
     dims = dict(hidden=hidden, inter=inter, n_experts=16, top_k=4)
     T = 400
     r = Run(dims, n_group=4, topk_group=2, seed=71, T=T)

@@ -1,8 +1,9 @@
 """Full-shape prefill (T = 4096, d = 6144, 256 experts top-8 + 1 shared) checked
 over every output.
 
-The prefill chunk runs the 192-row MFMA grouped GEMMs (512 weight rows per
-item), h entering the down projection as BF16 hi + lo halves.  Each batch is
+The prefill chunk runs the MFMA grouped GEMMs (gate/up on M tiles of 512
+weight rows, 192 rows, or 160 with FP32 activations; down on 192 x 384), h
+entering the down projection as BF16 hi + lo halves.  Each batch is
 checked three ways:
   * dispatch offsets and permutation bit-exact with the oracle's stable
     counting sort, every token's selection and routing weights bit-exact with
@@ -12,10 +13,11 @@ checked three ways:
     a share of the 1e-2 relative + 2e-3 absolute tolerance, which must stay
     below 0.8 (it measures ~0.01-0.03; an FP16 h measured 0.61 here with
     near-uniform routing and 1.1-1.7 with skewed weights);
-  * a token of every M tile of the dispatch (every routed expert's tiles,
-    all of a hot expert's and all 22 of the shared expert's) against the
-    oracle's own moeLayer restatement;
-  * (uniform and Zipf) bit for bit against the narrower 256 / 384-row tiles.
+  * a token of every M tile of both tile lists of the dispatch (every routed
+    expert's tiles, all of a hot expert's and all 22 / 26 of the shared
+    expert's) against the oracle's own moeLayer restatement;
+  * (uniform and Zipf) bit for bit against the narrower 192 x 256 gate/up
+    tiles.
 
 Routing: near-uniform (bias ~N(0, 0.001)), with BF16-valued and with FP32
 activations; skewed routing weights (a trained router's spread: tokens with
@@ -36,7 +38,7 @@ from moe_harness import (FULL, DeviceBackedLayer, Run, assert_close, layer_refer
 pytestmark = pytest.mark.gpu
 
 T, D, E, K = 4096, FULL["hidden"], FULL["n_experts"], FULL["top_k"]
-TILE = 192  # prefill M-tile rows at this size
+TILE, GU_TILE = 192, 160  # prefill M-tile rows at this size: down, gate/up
 
 
 @pytest.fixture(scope="module")
@@ -69,7 +71,8 @@ def check_every_output(host, xh, res, what):
 
 
 def check_tiles_against_oracle(host, xh, res, what):
-    picks = tile_cover_tokens(res["offsets"], res["perm"], T, K, TILE, 1)
+    picks = sorted(set(tile_cover_tokens(res["offsets"], res["perm"], T, K, TILE, 1)) |
+                   set(tile_cover_tokens(res["offsets"], res["perm"], T, K, GU_TILE, 1)))
     print(f"{what}: {len(picks)} tokens cover every M tile; oracle moeLayer on each", flush=True)
     for t in picks:
         ref = host.combine(xh[t], res["idx"][t], res["w"][t])
@@ -77,8 +80,8 @@ def check_tiles_against_oracle(host, xh, res, what):
 
 
 def narrow_tiles_agree(r, x, res, monkeypatch):
-    # The wide tiles (512 weight rows per item) accumulate every output in the
-    # same order as the narrower ones (256 gate/up, 384 down weight rows;
+    # The wide gate/up tiles (512 weight rows per item) accumulate every
+    # output in the same order as the narrower ones (192 x 256;
     # HFMOE_PREFILL_WIDE=0): K stage by stage, k half 0 then 1, hi then lo.
     monkeypatch.setenv("HFMOE_PREFILL_WIDE", "0")
     narrow = r.forward(x, T)

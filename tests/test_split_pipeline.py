@@ -42,7 +42,7 @@ def configs():
 def wide():
     line = [ln for ln in driver_lines() if ln.startswith("wide")]
     assert len(line) == 1
-    return dict(zip(["nad", "nwh", "after0", "after1"], map(int, line[0].split()[1:])))
+    return dict(zip(["nad", "nwh", "after", "wper1", "wper2"], map(int, line[0].split()[1:])))
 
 
 def simulate(c, nk, nad=None):
@@ -135,37 +135,50 @@ def test_a_count_that_is_one_too_large_is_caught(configs):
 
 def simulate_wide(w, H, nk, nad):
     """The wide gate/up tiles' issue sequence for one item (split_pipeline.h,
-    wide_after): a prologue of A(0) and weight half-stages 0, 1, 2, then per
-    sub-step j = H*s + half a wait, A(j + 1) (nad instructions) and, on a
-    stage's last sub-step, weight half-stages 2s + 3 and 2s + 4.  Every wait
-    must cover the loads the sub-step multiplies; the weight ring slots
-    refilled must not hold a half-stage still to be multiplied."""
+    wide_after, wide_w_per_substep): a prologue of A(0) and weight
+    half-stages 0, 1, 2, then per sub-step j = H*s + half a wait, A(j + 1)
+    (nad instructions) and weight half-stages 2s + 3 + half, ... (both on a
+    one-half stage, one per sub-step of a two-half stage).  The first sub-step
+    of a stage reads half-stages 2s and 2s + 1 from the ring (a second one
+    keeps their fragments).  Every wait must cover the loads the sub-step
+    multiplies; a ring slot refilled at a sub-step must hold no half-stage
+    that is still to be read (the sub-step's own reads come before its weight
+    DMAs)."""
     NWH = w["nwh"]
+    per = w["wper1"] if H == 1 else w["wper2"]
+    assert per * H == 2
     nj = nk * H
     seq = []
+    slot = {}  # ring slot -> half-stage it holds
 
     def issue(kind, i, n):
         if kind == "A" and i < nj or kind == "W" and i < 2 * nk:
             seq.append((kind, i, n))
+            if kind == "W":
+                held = slot.get(i % 3)
+                # the half-stage the slot held was read at its stage's first sub-step
+                assert held is None or 2 * (held // 2) <= 2 * s_now, (H, nk, i, held)
+                slot[i % 3] = i
 
+    s_now = -1
     issue("A", 0, nad)
     for q in range(3):
         issue("W", q, NWH)
     for j in range(nj):
         s, half = divmod(j, H)
+        s_now = s
         need = [("A", j)] + ([("W", 2 * s), ("W", 2 * s + 1)] if half == 0 else [])
+        if half == 0:
+            assert slot[(2 * s) % 3] == 2 * s and slot[(2 * s + 1) % 3] == 2 * s + 1
         idx = [next(i for i, (k, x, _) in enumerate(seq) if (k, x) == nd) for nd in need]
         after = sum(n for (_, _, n) in seq[max(idx) + 1:])
         steady = s + 1 < nk
-        allowed = (w["after0"] if half == 0 else w["after1"]) if (half == 1 or steady) else 0
+        allowed = w["after"] if steady else 0
         assert 0 <= allowed <= after, (H, nk, nad, j, allowed, after)
         issue("A", j + 1, nad)
-        if half == H - 1:
-            # slots of stage s's half-stages get the next ones; the half-stage
-            # in flight (2s + 2) keeps its own
-            assert {(2 * s + 3) % 3, (2 * s + 4) % 3} == {(2 * s) % 3, (2 * s + 1) % 3}
-            issue("W", 2 * s + 3, NWH)
-            issue("W", 2 * s + 4, NWH)
+        q0 = 2 * s + 3 + half + w.get("shift", 0)
+        for q in range(q0, q0 + per):
+            issue("W", q, NWH)
     assert all(x < (nj if k == "A" else 2 * nk) for k, x, _ in seq)
 
 
@@ -177,10 +190,19 @@ def test_wide_tiles_waits_are_safe(wide):
 
 
 def test_wide_tiles_one_more_outstanding_is_caught(wide):
-    # The first sub-step of a stage leaves exactly the last half-stage's DMAs
-    # outstanding: one more, and the wait no longer covers half-stage 2s + 1.
+    # A sub-step leaves exactly the last weight half-stage's DMAs outstanding:
+    # one more, and the wait no longer covers half-stage 2s + 1 (a first
+    # sub-step) or A(j) (a second one).
     for H in (1, 2):
         with pytest.raises(AssertionError):
-            simulate_wide(dict(wide, after0=wide["after0"] + 1), H, 4, wide["nad"])
+            simulate_wide(dict(wide, after=wide["after"] + 1), H, 4, wide["nad"])
     with pytest.raises(AssertionError):
-        simulate_wide(dict(wide, after1=wide["after1"] + 1), 2, 4, 0)
+        simulate_wide(dict(wide, after=wide["after"] + 1), 2, 4, 0)
+
+
+def test_wide_tiles_early_refill_is_caught(wide):
+    # Each weight half-stage one sub-step earlier goes into the slot of
+    # half-stage 2s + 2, not yet read.
+    for H in (1, 2):
+        with pytest.raises(AssertionError, match=r"^\(%d, 4, " % H):
+            simulate_wide(dict(wide, shift=-1), H, 4, wide["nad"])
