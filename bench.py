@@ -480,15 +480,16 @@ def run_grouped(args, workload: str, fp32_x: bool = False) -> dict:
     dom = kernels[dom_name]
     ai = dom["algorithmic_flops"] / dom["algorithmic_bytes"]
     summary = ("batched_t64" if workload == "batched" else "prefill_t4096") + "_hbm_traffic.md"
+    tkey = "traffic_bytes_per_launch" + ("_fp32_x" if fp32_x else "")
     extra = {"arithmetic_intensity": round(ai, 1), "mfma_tflops": dom["tflops"],
              "mfma_frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)}
     if ai < MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
         roof = {"bound": "hbm", "kernel": dom_name, "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(dom_name, summary), **extra}
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(dom_name, summary, tkey), **extra}
     else:
         roof = {"bound": "mfma", "kernel": dom_name, "achieved": dom["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": traffic_from_profile(dom_name, summary), **extra}
+                "traffic": traffic_from_profile(dom_name, summary, tkey), **extra}
     res = {
         "value": T / sec,
         "ms_per_step": sec * 1e3,
@@ -832,13 +833,15 @@ def run_copy(args) -> None:
     b.free()
 
 
-def traffic_from_profile(kernel: str, summary: str = "decode_t1_hbm_traffic.md") -> int | None:
-    """HBM bytes per launch of `kernel` from a committed counter summary."""
+def traffic_from_profile(kernel: str, summary: str = "decode_t1_hbm_traffic.md",
+                         key: str = "traffic_bytes_per_launch") -> int | None:
+    """HBM bytes per launch of `kernel` from a committed counter summary (the
+    line that starts with `key:`)."""
     path = os.path.join(ROOT, "profiles", summary)
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key + ":"):
             for item in line.split(":", 1)[1].split():
                 name, _, val = item.partition("=")
                 if name == kernel:
