@@ -83,3 +83,65 @@ def test_forward_replays_from_hip_graph(hf, T):
         for b in (x, x2, out_e, out_g):
             b.free()
         r.free()
+
+
+def test_replays_follow_the_activation_type(hf):
+    # One captured prefill-size forward (T = 1024: the wide gate/up tiles)
+    # replayed on FP32 activations, then BF16-valued ones, then FP32 again,
+    # written into the same input buffer between replays: the gate/up kernel
+    # picks its M tiles on the device from the x lo-half flag (160-row tiles
+    # with a lo half, 192-row without), so every replay must match the eager
+    # call on the same values bit for bit.
+    T, d = 1024, SMALL["hidden"]
+    r = Run(SMALL, n_group=8, topk_group=4, seed=88, T=T)
+    xb_dev = synth.make_x_dev(T, d, seed=88)
+    xb = xb_dev.download(np.float32, T * d)
+    xb_dev.free()
+    xf = (xb * (1.0 + np.float32(2.0 ** -10) * np.random.default_rng(88).standard_normal(xb.shape))).astype(
+        np.float32)
+    assert not np.array_equal(xf, xb)
+    xin = capi.DeviceBuffer.of(xf)
+    out = capi.DeviceBuffer(T * d * 4)
+    fwd = capi.load().hfmoe_moe_forward
+    h = hip()
+    s = C.c_void_p()
+    ok(h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        ref = {}
+        for name, xv in (("fp32", xf), ("bf16", xb)):
+            xin.upload(xv)
+            capi.check(fwd(0, xin.ptr, T, out.ptr, s))
+            ok(h.hipStreamSynchronize(s), "sync")
+            ref[name] = out.download(np.float32, T * d).copy()
+        assert not np.array_equal(ref["fp32"], ref["bf16"])
+
+        ok(h.hipStreamBeginCapture(s, CAPTURE_MODE_RELAXED), "hipStreamBeginCapture")
+        rc = fwd(0, xin.ptr, T, out.ptr, s)
+        ok(h.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
+        capi.check(rc)
+        ok(h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+
+        for rep, (name, xv) in enumerate((("fp32", xf), ("bf16", xb), ("fp32", xf), ("bf16", xb))):
+            xin.upload(xv)
+            capi.call("hfmoe_memset", out.ptr, 0, T * d * 4)
+            ok(h.hipGraphLaunch(exe, s), "hipGraphLaunch")
+            ok(h.hipStreamSynchronize(s), "sync")
+            got = out.download(np.float32, T * d)
+            assert np.array_equal(got.view(np.uint32), ref[name].view(np.uint32)), \
+                f"replay {rep} ({name} activations) differs from eager"
+        # Both eager results are the oracle's for a token (selection and tolerance).
+        for name, xv in (("fp32", xf), ("bf16", xb)):
+            xin.upload(xv)
+            res = r.forward(xin, T)
+            assert np.array_equal(res["out"].reshape(-1).view(np.uint32), ref[name].view(np.uint32))
+            r.check_token(xv.reshape(T, d)[0], res, 0)
+    finally:
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamDestroy(s)
+        for b in (xin, out):
+            b.free()
+        r.free()

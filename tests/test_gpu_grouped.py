@@ -131,15 +131,25 @@ PREFILL_EDGE = [
     # T = 800 gives 100 rows per expert on average (192-row tiles).
     ("partial_n_tiles_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 1),
     ("partial_n_tiles_no_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 0),
+    # inter 256: the wide gate/up tiles, 200 rows per expert (two 192-row
+    # tiles, or two 160-row ones with FP32 activations), with and without the
+    # shared expert's rows.
     ("top1_many_rows", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 1),
+    ("top1_many_rows_no_shared", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 0),
 ]
 
 
+@pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
 @pytest.mark.parametrize("name,dims,n_group,topk_group,n_shared", PREFILL_EDGE, ids=[e[0] for e in PREFILL_EDGE])
-def test_prefill_tiles_edge_shapes(hf, name, dims, n_group, topk_group, n_shared):
+def test_prefill_tiles_edge_shapes(hf, name, dims, n_group, topk_group, n_shared, fp32_x):
     T = 800
     r = Run(dims, n_group=n_group, topk_group=topk_group, seed=95, T=T, n_shared=n_shared)
     x = synth.make_x_dev(T, dims["hidden"], seed=95)
+    if fp32_x:  # not BF16-valued: the x lo half is multiplied too
+        xv = x.download(np.float32, T * dims["hidden"])
+        x.free()
+        x = capi.DeviceBuffer.of((xv * (1.0 + np.float32(2.0 ** -10) *
+                                        np.random.default_rng(95).standard_normal(xv.shape))).astype(np.float32))
     res = r.forward(x, T)
     xh = x.download(np.float32, T * dims["hidden"]).reshape(T, -1)
     counts = check_dispatch(res, dims["n_experts"])
