@@ -40,10 +40,10 @@ int gemm_blocks(int tile_rows) {
     return env_int("HFMOE_GEMM_BLOCKS", tile_rows == kGemmTileRows ? g.num_cus * 2 : g.num_cus);
 }
 
-// Prefill tiles (192 rows) once experts average 96+ rows: an expert's rows
-// then fit one tile, its weights stream through the memory system once, and
-// each activation row is requested once per 512 (gate/up, the wide tiles) or
-// 384 (down) weight rows.
+// Prefill tiles (192 rows; the wide tiles' own list 160) once experts
+// average 96+ rows: an expert's rows then fit one tile, its weights stream
+// through the memory system once, and each activation row is requested once
+// per 512 weight rows (the wide tiles; 256 or 384 on the split tiles).
 static int expert_tile_rows(int T) {
     const Cfg& c = g.cfg;
     return (size_t)T * c.k >= (size_t)96 * c.E ? kPrefillTileRows : kGemmTileRows;
@@ -116,9 +116,9 @@ int grouped_tile_rows(int T) { return expert_tile_rows(T); }
 // The prefill gate/up GEMM takes the wide tiles (512 weight rows, 256
 // outputs of h; 192 rows, or 160 from a second tile list when x has a lo
 // half) when the intermediate size is a multiple of 256, unless
-// HFMOE_PREFILL_WIDE=0 (192 x 256 tiles): the down projection keeps its 192 x
-// 384 tiles, on which its two halves of h cost fewer LDS reads per weight
-// byte.
+// HFMOE_PREFILL_WIDE=0 (192 x 256 tiles, and 192 x 384 for the down
+// projection, which otherwise takes 160 x 512 tiles from the second list
+// when hidden is a multiple of 512).
 static bool prefill_wide(int TR) {
     return TR == kPrefillTileRows && g.cfg.I % (kWideTileCols / 2) == 0 && env_int("HFMOE_PREFILL_WIDE", 1) != 0;
 }
@@ -215,15 +215,19 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
 
     // Down projections of every group; row r's output lands at row perm[r] of
     // y: pair slot t*k + r for routed rows, T*k + t for the shared expert.
+    // The wide down tiles (160 rows x 512 weight rows, on the gate/up's
+    // 160-row list) when hidden is a multiple of 512, unless
+    // HFMOE_DOWN_WIDE=0 (192 x 384).
+    const bool dn_wide = wide && c.d % kWideTileCols == 0 && env_int("HFMOE_DOWN_WIDE", 1) != 0;
     GemmArgs dn{};
     dn.K = c.I;
     dn.N = c.d;
-    dn.tile_rows = TR;
-    dn.tile_cols = gemm_tile_cols(TR, EPI_SCATTER);
+    dn.tile_rows = dn_wide ? kWideTileRows : TR;
+    dn.tile_cols = dn_wide ? kWideTileCols : gemm_tile_cols(TR, EPI_SCATTER);
     dn.n_tiles = gemm_n_tiles(EPI_SCATTER, c.d, dn.tile_cols);
-    dn.tile_group = w.tile_expert;
-    dn.tile_row0 = w.tile_row0;
-    dn.ntiles_dev = w.ntiles;
+    dn.tile_group = dn_wide ? w.tile_expert_gu : w.tile_expert;
+    dn.tile_row0 = dn_wide ? w.tile_row0_gu : w.tile_row0;
+    dn.ntiles_dev = dn_wide ? w.ntiles + 32 : w.ntiles;
     dn.group_end = w.offsets + 1;
     dn.rows_total = P + shared_rows;
     dn.a_hi = w.hh;
@@ -235,7 +239,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
-    dn.shared_mtiles = gu.shared_mtiles;
+    dn.shared_mtiles = dn_wide ? gu.lo_tiles.shared_mtiles : gu.shared_mtiles;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;

@@ -24,14 +24,14 @@
 //     memory into an LDS ring by DMA (global_load_lds_dwordx4), A fragments
 //     straight into registers (L2-resident activations, row-gathered through
 //     a_rowmap), both 2-4 K stages ahead of the one multiplied;
-//   * 192 (M) x 256 or 384 (N) x 64 (K), 8 wavefronts (prefill down
-//     projection, dense layers, LM head): both operands by DMA into LDS,
-//     wavefronts split 2 (row-block parity) x 4 (column groups) --
-//     gemm_item_split below;
+//   * 192 (M) x 256 or 384 (N) x 64 (K), 8 wavefronts (prefill GEMMs whose
+//     sizes do not fit the wide tiles, dense layers, LM head): both operands
+//     by DMA into LDS, wavefronts split 2 (row-block parity) x 4 (column
+//     groups) -- gemm_item_split below;
 //   * 192 or 160 (M) x 512 (N) x 64 (K), 8 wavefronts of 64 weight rows each
-//     over all rows (prefill gate/up; 160-row tiles when x has a lo half):
-//     weights through private per-wavefront LDS rings -- gemm_item_wide
-//     below.
+//     over all rows (prefill gate/up, 160-row tiles when x has a lo half;
+//     prefill down projection, 160-row tiles): weights through private
+//     per-wavefront LDS rings -- gemm_item_wide below.
 // Persistent workgroups walk per-XCD item lists, n fastest, so an M tile's
 // activations are reused within that XCD's L2 (item_range).
 //
@@ -953,15 +953,17 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// Wide prefill gate/up tiles: 192 (M) x 512 (N: 256 gate + 256 up weight
-// rows) x 64 (K), or 160 x 512 x 64 when x has a lo half, eight wavefronts,
-// one workgroup per CU.
+// Wide prefill tiles: gate/up 192 (M) x 512 (N: 256 gate + 256 up weight
+// rows) x 64 (K), or 160 x 512 x 64 when x has a lo half; the down projection
+// 160 x 512 x 64 (h: always two halves).  Eight wavefronts, one workgroup per
+// CU.
 //
-// What bounds the prefill gate/up GEMM is the CU's stream of line requests to
-// L2: the weights once, plus the activation rows once per N tile.  Per weight
+// What bounds the prefill GEMMs is the CU's stream of line requests to L2:
+// the weights once, plus the activation rows once per N tile.  Per weight
 // byte the activations add rows x halves / N; 512 weight rows per tile instead
-// of 256 cut that from 0.56 to 0.28 (BF16-valued x) and from 1.12 to 0.56
-// (FP32 x: hi and lo halves).  Registers and LDS set the layout:
+// of 256 cut that from 0.56 to 0.28 (gate/up, BF16-valued x) and from 1.12
+// to 0.56 (FP32 x: hi and lo halves), and instead of the down projection's
+// 384 from 0.75 to about 0.5.  Registers and LDS set the layout:
 //   * wavefront w owns weight rows [64 w, 64 w + 64) of the tile (32 gate
 //     rows then the 32 matching up rows) and all rows of the M tile: up to
 //     12 x 4 accumulator blocks, 192 of its 256 registers, and no weight
@@ -982,9 +984,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_split_kernel(GemmArgs a) 
 // With one half of A the 192-row tiles measure faster (fewer shared-expert
 // tiles); the 160-row ones still hold a near-uniform prefill's ~128-row
 // experts in one tile.  The cost of this layout is LDS reads: every
-// wavefront reads all rows' activation fragments; the down projection's two
-// halves of h would cost more LDS reads per weight byte here than on its
-// 384-row tiles, which therefore stay.
+// wavefront reads all rows' activation fragments (with the weight fragments
+// kept for the second half, about 5 bytes per weight byte, as on the 384-row
+// split tiles).
 constexpr int kWideWaves = 8;
 constexpr int kWideWaveRows = kWideTileCols / kWideWaves;  // weight rows per wavefront
 constexpr int kWideHalfRows = kWideWaveRows / 2;           // weight rows per half-stage
@@ -1003,9 +1005,14 @@ static_assert(kWideLds + 64 <= 160 * 1024, "wide LDS");
 // else 2s + 3 from the first sub-step and 2s + 4 from the second.  Loads
 // complete in issue order, so a sub-step may leave exactly the last weight
 // half-stage issued before it outstanding (split_pipeline.h: wide_after).
-template <int HALVES, class Setup>
+// EPI_SWIGLU: the gate/up GEMM (x, one or two halves); EPI_SCATTER: the down
+// projection (h, two halves), each wavefront's 64 weight rows 64 consecutive
+// output columns (half-stage h: rows 32 h + [0, 32) of them).
+template <int EPI, int HALVES, class Setup>
 __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint16_t* lds, int t, int wave,
                                                Setup&& on_setup) {
+    static_assert(EPI == EPI_SWIGLU || (EPI == EPI_SCATTER && HALVES == 2), "wide tiles");
+    constexpr bool SW = EPI == EPI_SWIGLU;
     constexpr int ROWS = HALVES == 1 ? kPrefillTileRows : kWideTileRows;
     constexpr int AST = ROWS * GBK;                 // elements per A sub-step slot
     constexpr int NAD = (ROWS / 8 + kWideWaves - 1) / kWideWaves;  // A DMAs (8 rows x 128 bytes) per wavefront
@@ -1031,9 +1038,9 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     const int row_end = __builtin_amdgcn_readfirstlane(a.group_end ? a.group_end[g] : a.rows_total);
     const int rows = min(ROWS, row_end - row0);
     const int nrb = (rows + 15) >> 4;
-    const int n0 = nt * (kWideTileCols / 2);  // first h column of the tile
-    const uint16_t* b0 = a.b_tab ? a.b_tab[3 * g + a.b_which] : a.b_fixed0;      // gate rows
-    const uint16_t* b1 = a.b_tab ? a.b_tab[3 * g + a.b_which + 1] : a.b_fixed1;  // up rows
+    const int n0 = nt * (SW ? kWideTileCols / 2 : kWideTileCols);  // first output column of the tile
+    const uint16_t* b0 = a.b_tab ? a.b_tab[3 * g + a.b_which] : a.b_fixed0;  // gate (down) rows
+    const uint16_t* b1 = !SW ? b0 : a.b_tab ? a.b_tab[3 * g + a.b_which + 1] : a.b_fixed1;  // up rows
 
     // DMA lane l of an 8-row block loads chunk (l & 7) ^ (l >> 3) of block row
     // l >> 3, so 16-byte chunk c of slot row r sits at position c ^ (r & 7):
@@ -1052,8 +1059,9 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
         aoff[i] = (uint32_t)(2 * (src * a.K + dc * 8));
     }
     // Weights: half-stage h of this wavefront is gate rows (h = 0) or the
-    // matching up rows (h = 1) n0 + 32 w + [0, 32); DMA i covers 8 of them.
-    const int wrow = n0 + kWideHalfRows * wave + dr;
+    // matching up rows (h = 1) n0 + 32 w + [0, 32), or down rows
+    // n0 + 64 w + 32 h + [0, 32); DMA i covers 8 of them.
+    const int wrow = n0 + (SW ? kWideHalfRows : kWideWaveRows) * wave + dr;
     const uint32_t woff = (uint32_t)(2 * ((size_t)wrow * a.b_ld + dc * 8));
     const __amdgpu_buffer_rsrc_t rw0 = raw_rsrc(uniform_ptr(b0));
     const __amdgpu_buffer_rsrc_t rw1 = raw_rsrc(uniform_ptr(b1));
@@ -1075,7 +1083,8 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     auto issue_w1 = [&](int q, int i) {
         if (q >= 2 * nk) return;
         const int s = q >> 1, h = q & 1;
-        dma16(pick(h != 0, rw1, rw0), woff, (uint32_t)s * (2 * GBK) + (uint32_t)(8 * i) * wrow_bytes,
+        dma16(pick(h != 0, rw1, rw0), woff,
+              (uint32_t)s * (2 * GBK) + (uint32_t)(8 * i + (SW ? 0 : kWideHalfRows * h)) * wrow_bytes,
               wring + (q % kWideWRing) * WHS + i * 512);
     };
     auto issue_w = [&](int q) {
@@ -1202,12 +1211,14 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
             compute(aring + (j & 1) * AST, s, first, j + 1, nab, 2 * s + 3 + (first ? 0 : 1));
         }
         // Every load of the item has landed (the last stage waits for all).
-        // h columns n0 + 32 w + 16 cb + 4 fq + q from gate block cb and up block cb + 2.
-        const int col0 = n0 + kWideHalfRows * wave + 4 * fq;
+        // SWIGLU: h columns n0 + 32 w + 16 cb + 4 fq + q from gate block cb
+        // and up block cb + 2; SCATTER: y columns n0 + 64 w + 16 cb + 4 fq + q.
+        const int col0 = n0 + (SW ? kWideHalfRows : kWideWaveRows) * wave + 4 * fq;
 #pragma unroll
         for (int j = 0; j < NM; ++j) {
             const int rl = 16 * j + fr;
-            if (rl < rows) store_tile_row<EPI_SWIGLU, CB>(a, acc[j], row0 + rl, col0, 0, row0 + rl);
+            if (rl < rows)
+                store_tile_row<EPI, CB>(a, acc[j], row0 + rl, col0, 0, SW ? row0 + rl : a.scatter_rows[row0 + rl]);
         }
     };
     // Row-block counts in buckets (8 .. 12 or 10 exact, the near-uniform
@@ -1222,10 +1233,12 @@ __device__ __forceinline__ void gemm_item_wide(const GemmArgs& a, int item, uint
     });
 }
 
-// x (BF16 hi, and lo when the device flag says x is not BF16-valued) times
-// the gate and up weights, h = silu(g) * u out as BF16 hi / lo.  With the lo
-// half the items are those of the 160-row M tiles (GemmArgs::lo_tiles),
-// else of the 192-row ones.
+// EPI_SWIGLU: x (BF16 hi, and lo when the device flag says x is not
+// BF16-valued) times the gate and up weights, h = silu(g) * u out as BF16
+// hi / lo; with the lo half the items are those of the 160-row M tiles
+// (GemmArgs::lo_tiles), else of the 192-row ones.  EPI_SCATTER: h (hi and lo)
+// times the down weights on the launch's own 160-row tiles, y rows scattered.
+template <int EPI>
 __global__ __launch_bounds__(64 * kWideWaves, 1) void grouped_gemm_wide_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t wlds[];  // kWideLds bytes
     const int t = threadIdx.x;
@@ -1241,7 +1254,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void grouped_gemm_wide_kernel(G
                 on_setup();
                 return;
             }
-            gemm_item_wide<HALVES>(b, item, wlds, t, wave, on_setup);
+            gemm_item_wide<EPI, HALVES>(b, item, wlds, t, wave, on_setup);
             lds_barrier();
         };
         if (!b.item_ctr || !r.by_mtile) {
@@ -1250,7 +1263,9 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void grouped_gemm_wide_kernel(G
         }
         dynamic_items(b, r, run);
     };
-    if (*a.a_lo_flag != 0u) {
+    if constexpr (EPI == EPI_SCATTER) {
+        items(a, std::integral_constant<int, 2>{});
+    } else if (*a.a_lo_flag != 0u) {
         GemmArgs b = a;
         b.tile_rows = kWideTileRows;
         b.tile_group = a.lo_tiles.group;
@@ -1414,26 +1429,33 @@ static hipError_t launch_gemm_split(const GemmArgs& a, int blocks, hipStream_t s
     return launch(grouped_gemm_split_kernel<EPI, LOM, ROWS>, dim3(blocks), dim3(512), (uint32_t)lds, s, a);
 }
 
+template <int EPI>
 static hipError_t launch_gemm_wide(const GemmArgs& a, int blocks, hipStream_t s) {
     static bool raised = false;
     if (!raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(grouped_gemm_wide_kernel<EPI>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLds);
         if (e != hipSuccess) return e;
         raised = true;
     }
-    return launch(grouped_gemm_wide_kernel, dim3(blocks), dim3(64 * kWideWaves), (uint32_t)kWideLds, s, a);
+    return launch(grouped_gemm_wide_kernel<EPI>, dim3(blocks), dim3(64 * kWideWaves), (uint32_t)kWideLds, s, a);
 }
 
 template <int EPI, int LOM>
 static hipError_t launch_shape(const GemmArgs& a, int blocks, hipStream_t s) {
-    if (a.tile_rows == kPrefillTileRows && a.tile_cols == kWideTileCols) {
-        // The MoE gate/up GEMM only (on x, whose lo half goes by the device
-        // flag, and with the 160-row tile list for it), whole wide tiles
+    if (a.tile_cols == kWideTileCols) {
+        // The MoE gate/up GEMM (on x, whose lo half goes by the device flag,
+        // with the 160-row tile list for it) on 192-row tiles, and the MoE
+        // down projection (h, both halves) on 160-row tiles: whole wide tiles
         // (their weight DMAs are not clamped at N), one K split.
         if constexpr (EPI == EPI_SWIGLU && LOM == kLoByFlag) {
-            if (a.N % (kWideTileCols / 2) == 0 && a.ksplit == 1 && a.a_lo_flag && a.lo_tiles.count)
-                return launch_gemm_wide(a, blocks, s);
+            if (a.tile_rows == kPrefillTileRows && a.N % (kWideTileCols / 2) == 0 && a.ksplit == 1 &&
+                a.a_lo_flag && a.lo_tiles.count)
+                return launch_gemm_wide<EPI_SWIGLU>(a, blocks, s);
+        }
+        if constexpr (EPI == EPI_SCATTER && LOM == kLoAlways) {
+            if (a.tile_rows == kWideTileRows && a.N % kWideTileCols == 0 && a.ksplit == 1 && a.scatter_rows)
+                return launch_gemm_wide<EPI_SCATTER>(a, blocks, s);
         }
         return hipErrorInvalidValue;
     }

@@ -13,9 +13,10 @@ constexpr int kGemmTileK = 64;      // K per pipeline stage (K % (64 * ksplit) =
 
 enum GemmEpi { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 
-// Weight rows per tile of the wide prefill gate/up kernel (eight wavefronts
-// of 64 weight rows, 32 gate + 32 up, each over all rows of an M tile), and
-// the rows of its M tiles when x has a lo half (GemmArgs::lo_tiles).
+// Weight rows per tile of the wide prefill kernel (eight wavefronts of 64
+// weight rows, 32 gate + 32 up or 64 down rows, each over all rows of an M
+// tile), and the rows of its M tiles when A has a lo half: x in the gate/up
+// GEMM (GemmArgs::lo_tiles), h in the down projection.
 constexpr int kWideTileCols = 512, kWideTileRows = 160;
 
 // Weight rows per tile for M tiles of tile_rows rows (MoE prefill: gate/up
@@ -125,8 +126,8 @@ struct TileList {
     int* count = nullptr;
 };
 // tl0: the M tiles of both grouped GEMMs; tl1 (when tl1.rows > 0): a second
-// list of the same groups, the wide gate/up kernel's tiles when x has a lo
-// half (GemmArgs::lo_tiles).
+// list of the same groups, the wide kernel's tiles for the down projection
+// and, when x has a lo half, for the gate/up GEMM (GemmArgs::lo_tiles).
 hipError_t launch_dispatch(const int* idx, int T, int k, int E, const TileList& tl0, const TileList& tl1,
                            int shared_rows, int* counts, int* offsets, int* perm, int* row_token, int* chunk_hist,
                            unsigned* item_ctr, hipStream_t s);

@@ -131,9 +131,9 @@ PREFILL_EDGE = [
     # T = 800 gives 100 rows per expert on average (192-row tiles).
     ("partial_n_tiles_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 1),
     ("partial_n_tiles_no_shared", dict(hidden=960, inter=320, n_experts=32, top_k=4), 4, 2, 0),
-    # inter 256: the wide gate/up tiles, 200 rows per expert (two 192-row
-    # tiles, or two 160-row ones with FP32 activations), with and without the
-    # shared expert's rows.
+    # inter 256, hidden 512: the wide tiles, 200 rows per expert (gate/up on
+    # two 192-row tiles, or two 160-row ones with FP32 activations; down on
+    # two 160-row tiles), with and without the shared expert's rows.
     ("top1_many_rows", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 1),
     ("top1_many_rows_no_shared", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 0),
 ]
@@ -141,7 +141,7 @@ PREFILL_EDGE = [
 
 @pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
 @pytest.mark.parametrize("name,dims,n_group,topk_group,n_shared", PREFILL_EDGE, ids=[e[0] for e in PREFILL_EDGE])
-def test_prefill_tiles_edge_shapes(hf, name, dims, n_group, topk_group, n_shared, fp32_x):
+def test_prefill_tiles_edge_shapes(hf, monkeypatch, name, dims, n_group, topk_group, n_shared, fp32_x):
     T = 800
     r = Run(dims, n_group=n_group, topk_group=topk_group, seed=95, T=T, n_shared=n_shared)
     x = synth.make_x_dev(T, dims["hidden"], seed=95)
@@ -159,6 +159,13 @@ def test_prefill_tiles_edge_shapes(hf, name, dims, n_group, topk_group, n_shared
     for t in range(0, T, 41):
         r.check_token(xh[t], res, t)
     check_vs_decode(r, x, res, range(3, T, 160), dims["hidden"])
+    if dims["inter"] % 256 == 0:
+        # The wide tiles (gate/up; down too when hidden is a multiple of 512)
+        # against the narrow ones, bit for bit.
+        monkeypatch.setenv("HFMOE_PREFILL_WIDE", "0")
+        narrow = r.forward(x, T)
+        monkeypatch.delenv("HFMOE_PREFILL_WIDE")
+        assert np.array_equal(res["out"].view(np.uint32), narrow["out"].view(np.uint32))
     x.free()
     r.free()
 

@@ -1,9 +1,9 @@
 """Full-shape prefill (T = 4096, d = 6144, 256 experts top-8 + 1 shared) checked
 over every output.
 
-The prefill chunk runs the MFMA grouped GEMMs (gate/up on M tiles of 512
-weight rows, 192 rows, or 160 with FP32 activations; down on 192 x 384), h
-entering the down projection as BF16 hi + lo halves.  Each batch is
+The prefill chunk runs the MFMA grouped GEMMs on M tiles of 512 weight rows
+(gate/up on 192 rows, or 160 with FP32 activations; down on 160), h entering
+the down projection as BF16 hi + lo halves.  Each batch is
 checked three ways:
   * dispatch offsets and permutation bit-exact with the oracle's stable
     counting sort, every token's selection and routing weights bit-exact with
@@ -16,8 +16,8 @@ checked three ways:
   * a token of every M tile of both tile lists of the dispatch (every routed
     expert's tiles, all of a hot expert's and all 22 / 26 of the shared
     expert's) against the oracle's own moeLayer restatement;
-  * (uniform and Zipf) bit for bit against the narrower 192 x 256 gate/up
-    tiles.
+  * (uniform and Zipf) bit for bit against the narrower tiles (192 x 256
+    gate/up, 192 x 384 down).
 
 Routing: near-uniform (bias ~N(0, 0.001)), with BF16-valued and with FP32
 activations; skewed routing weights (a trained router's spread: tokens with
@@ -38,7 +38,7 @@ from moe_harness import (FULL, DeviceBackedLayer, Run, assert_close, layer_refer
 pytestmark = pytest.mark.gpu
 
 T, D, E, K = 4096, FULL["hidden"], FULL["n_experts"], FULL["top_k"]
-TILE, GU_TILE = 192, 160  # prefill M-tile rows at this size: down, gate/up
+TILE, GU_TILE = 192, 160  # prefill M-tile rows at this size: the two tile lists
 
 
 @pytest.fixture(scope="module")
@@ -80,9 +80,9 @@ def check_tiles_against_oracle(host, xh, res, what):
 
 
 def narrow_tiles_agree(r, x, res, monkeypatch):
-    # The wide gate/up tiles (512 weight rows per item) accumulate every
-    # output in the same order as the narrower ones (192 x 256;
-    # HFMOE_PREFILL_WIDE=0): K stage by stage, k half 0 then 1, hi then lo.
+    # The wide tiles (512 weight rows per item) accumulate every output in
+    # the same order as the narrower ones (192 x 256 gate/up, 192 x 384 down;
+    # HFMOE_PREFILL_WIDE=0): K stage by stage, hi then lo, k half 0 then 1.
     monkeypatch.setenv("HFMOE_PREFILL_WIDE", "0")
     narrow = r.forward(x, T)
     monkeypatch.delenv("HFMOE_PREFILL_WIDE")

@@ -24,11 +24,14 @@ def run_cases(cases):
 
 def test_dealing_of_the_benchmark_shapes():
     # prefill T = 4096: 256 routed M tiles + 22 shared (192 rows), 8 N tiles
-    # for gate/up (256 h columns) and 16 for down (384 columns); gate/up on
-    # its 160-row list, 256 + 26 M tiles and 8 N tiles (256 h columns); a
-    # Zipf batch with multi-tile hot experts; no shared expert.
-    run_cases([(278, 8, 8, 22, 1), (278, 16, 8, 22, 2), (282, 8, 8, 26, 1), (300, 8, 8, 22, 1),
-               (300, 16, 8, 22, 2), (310, 8, 8, 26, 1), (256, 16, 8, 0, 0), (9, 16, 8, 1, 2)])
+    # for gate/up (256 h columns) and 16 for down (384 columns); on the
+    # 160-row list, 256 + 26 M tiles and 8 N tiles for gate/up (256 h
+    # columns), 12 for down (512 columns: 12 N tiles do not split over 8
+    # XCDs, so the shared tiles are dealt whole); a Zipf batch with
+    # multi-tile hot experts; no shared expert.
+    run_cases([(278, 8, 8, 22, 1), (278, 16, 8, 22, 2), (282, 8, 8, 26, 1), (282, 12, 8, 0, 0),
+               (300, 8, 8, 22, 1), (300, 16, 8, 22, 2), (310, 8, 8, 26, 1), (310, 12, 8, 0, 0),
+               (256, 16, 8, 0, 0), (9, 16, 8, 1, 2)])
 
 
 def test_dealing_of_random_shapes():
