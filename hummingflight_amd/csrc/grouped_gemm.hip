@@ -175,10 +175,10 @@ struct ItemRange {
     bool by_ntile;
     int n0, n_local, m0, m_cnt, ksplit;
     // Dynamic by_mtile dealing (item_deal.h), the shared expert's last
-    // sh_m M tiles dealt by blocks of sh_nl N tiles (GemmArgs::shared_mtiles;
+    // sh_m M tiles dealt by blocks of N tiles (GemmArgs::shared_mtiles;
     // 0: none).
-    int m_tiles, sh_m, sh_nl;
-    __device__ __forceinline__ XcdDeal deal() const { return XcdDeal{m_tiles, per_m, nxcd, sh_m, sh_nl}; }
+    int m_tiles, sh_m;
+    __device__ __forceinline__ XcdDeal deal() const { return XcdDeal{m_tiles, per_m, nxcd, sh_m}; }
     __device__ __forceinline__ int item(int li) const {
         if (by_ntile) {
             const int per_n = m_cnt * ksplit;
@@ -212,10 +212,8 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
     }
     r.by_mtile = !r.by_ntile && DEAL_M && m_tiles >= r.nxcd;
     r.m_tiles = m_tiles;
-    const bool sh = r.by_mtile && a.item_ctr && a.ksplit == 1 && a.shared_mtiles > 0 &&
-                    a.shared_mtiles <= m_tiles && a.n_tiles % r.nxcd == 0;
+    const bool sh = r.by_mtile && a.item_ctr && a.ksplit == 1 && a.shared_mtiles > 0 && a.shared_mtiles <= m_tiles;
     r.sh_m = sh ? a.shared_mtiles : 0;
-    r.sh_nl = sh ? a.n_tiles / r.nxcd : 0;
     const int local = blockIdx.x / r.nxcd;
     if (r.by_ntile) {
         r.begin = local;
