@@ -136,6 +136,12 @@ PREFILL_EDGE = [
     # two 160-row tiles), with and without the shared expert's rows.
     ("top1_many_rows", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 1),
     ("top1_many_rows_no_shared", dict(hidden=512, inter=256, n_experts=4, top_k=1), 1, 1, 0),
+    # hidden 768 (not a multiple of 512): wide gate/up tiles (inter 512: two
+    # N tiles), the down projection on 192 x 384 split tiles (two N tiles);
+    # hidden 1536: the wide down tiles with 3 N tiles, fewer than the 8 XCDs
+    # (the shared expert's tiles dealt to 3 of them, the rest taken across).
+    ("wide_gateup_split_down", dict(hidden=768, inter=512, n_experts=16, top_k=4), 4, 2, 1),
+    ("wide_down_three_n_tiles", dict(hidden=1536, inter=256, n_experts=16, top_k=4), 4, 2, 1),
 ]
 
 
