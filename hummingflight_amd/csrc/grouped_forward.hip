@@ -158,7 +158,8 @@ int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     HF_CHECK_LAUNCH(launch_select(g.ws.scores, T, c, g.ws.idx, g.ws.wts, s), "select");
     prof_begin(p, "dispatch", s);
     TileList tl{TR, w.tile_expert, w.tile_row0, w.ntiles}, tl_gu{};
-    if (prefill_wide(TR)) tl_gu = TileList{kWideTileRows, w.tile_expert_gu, w.tile_row0_gu, w.ntiles + 32};
+    w.wide = prefill_wide(TR);
+    if (w.wide) tl_gu = TileList{kWideTileRows, w.tile_expert_gu, w.tile_row0_gu, w.ntiles + 32};
     HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, tl, tl_gu, shared_rows, w.counts, w.offsets, w.perm,
                                     w.row_token, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
                     "dispatch");
@@ -174,8 +175,9 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     Pending p;
 
     // Gate/up of every group: the routed experts' (token, rank) rows and the
-    // shared expert's token rows (group E), one launch.
-    const bool wide = prefill_wide(TR);
+    // shared expert's token rows (group E), one launch.  The wide tiles when
+    // the dispatch of this batch wrote their tile list.
+    const bool wide = w.wide && TR == kPrefillTileRows;
     GemmArgs gu{};
     gu.K = c.d;
     gu.N = c.I;

@@ -39,8 +39,9 @@ struct GroupedWorkspace {
     int* tile_expert = nullptr;  // [max_tiles] group of each M tile
     int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
     int* ntiles = nullptr;       // [64] M tiles in use: [0] this list, [32] the wide gate/up list
-    int* tile_expert_gu = nullptr;  // [max_tiles] the wide gate/up tiles (kWideTileRows rows)
+    int* tile_expert_gu = nullptr;  // [max_tiles] the wide kernel's tiles (kWideTileRows rows)
     int* tile_row0_gu = nullptr;
+    bool wide = false;              // the last dispatch wrote that list (the GEMMs after it take the wide tiles)
     int* chunk_hist = nullptr;   // [kDispatchMaxChunks, E] dispatch chunk counts / first slots
     unsigned* item_ctr = nullptr;  // [kItemCounters] prefill GEMM work counters (zeroed by the dispatch)
     unsigned int* lo_flag = nullptr;  // [0] x has a nonzero BF16 lo half
