@@ -426,7 +426,8 @@ def profiled_pass(step, steps: int) -> tuple[dict, float]:
 
 
 def run_grouped(args, workload: str, fp32_x: bool = False) -> dict:
-    """Batched decode (T=64, Zipf routing) or a prefill chunk (T=4096).
+    """Batched decode (T=64, Zipf routing) or a prefill chunk (T=4096, or
+    --tokens, near-uniform routing).
 
     fp32_x: activations that are not BF16-valued (BF16 values scaled by
     1 + 2^-10 N(0, 1), FP32 like the reference's RMSNorm output), which the
@@ -440,7 +441,7 @@ def run_grouped(args, workload: str, fp32_x: bool = False) -> dict:
         layer_kw = dict(bias=np.array(zb["bias"], np.float32))
         routing = "correction bias calibrated for Zipf(1.1) expert popularity"
     else:
-        T = 4096
+        T = args.tokens
         seed = args.seed
         layer_kw = dict(bias_std=0.001)
         routing = "near-uniform, correction bias ~N(0,0.001)"
@@ -479,7 +480,9 @@ def run_grouped(args, workload: str, fp32_x: bool = False) -> dict:
     dom_name = max((n for n in algo if n in kernels), key=lambda n: kernels[n]["avg_us"])
     dom = kernels[dom_name]
     ai = dom["algorithmic_flops"] / dom["algorithmic_bytes"]
-    summary = ("batched_t64" if workload == "batched" else "prefill_t4096") + "_hbm_traffic.md"
+    # counter summaries exist for T = 64 (batched) and T = 4096 (prefill) only
+    summary = "batched_t64_hbm_traffic.md" if workload == "batched" else \
+        "prefill_t4096_hbm_traffic.md" if T == 4096 else ""
     tkey = "traffic_bytes_per_launch" + ("_fp32_x" if fp32_x else "")
     extra = {"arithmetic_intensity": round(ai, 1), "mfma_tflops": dom["tflops"],
              "mfma_frac": round(dom["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)}
@@ -838,7 +841,7 @@ def traffic_from_profile(kernel: str, summary: str = "decode_t1_hbm_traffic.md",
     """HBM bytes per launch of `kernel` from a committed counter summary (the
     line that starts with `key:`)."""
     path = os.path.join(ROOT, "profiles", summary)
-    if not os.path.exists(path):
+    if not summary or not os.path.isfile(path):
         return None
     for line in open(path):
         if line.startswith(key + ":"):
@@ -878,7 +881,7 @@ def run_configs(args, cpu_tokens_per_s: float | None = None) -> dict:
     out = {}
     for name, fn, steps, warm in runs:
         a = copy.copy(args)
-        a.steps, a.warmup, a.no_cpu_baseline = steps, warm, True
+        a.steps, a.warmup, a.no_cpu_baseline, a.tokens = steps, warm, True, 4096
         t0 = time.perf_counter()
         r = fn(a)
         keep = {"tokens_per_s": round(r["value"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps,
@@ -923,6 +926,8 @@ def main() -> int:
                     help="streamed: pin experts within 10%% of the layer's top routing weight (setRouterPrefetch)")
     ap.add_argument("--dense-tokens", type=int, default=1, help="dense: tokens per call")
     ap.add_argument("--prefill-tokens", type=int, default=4096, help="streamed_prefill: tokens per call")
+    ap.add_argument("--tokens", type=int, default=4096,
+                    help="prefill: tokens per call (near-uniform routing at any batch size, 2 or more)")
     ap.add_argument("--load-experts", type=int, default=64,
                     help="load: routed experts in the written checkpoint layer (75.5 MB each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -964,7 +969,10 @@ def main() -> int:
         res = run_streamed_prefill(args)
     else:
         res = run_grouped(args, args.workload, fp32_x=args.fp32_x)
-    line = {"metric": METRICS[args.workload], "value": round(res.pop("value"), 2), "unit": "tokens/s",
+    metric = METRICS[args.workload]
+    if args.workload == "prefill" and args.tokens != 4096:
+        metric = metric.replace("T=4096", f"T={args.tokens}")
+    line = {"metric": metric, "value": round(res.pop("value"), 2), "unit": "tokens/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(res.pop("ms_per_step"), 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic", **res}

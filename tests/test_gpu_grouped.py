@@ -44,8 +44,10 @@ def check_vs_decode(r, x, res, tokens, d):
     assert same >= len(tokens) - 1
 
 
-@pytest.mark.parametrize("T", [2, 37, 130])
+@pytest.mark.parametrize("T", [2, 24, 130])
 def test_grouped_small(hf, T):
+    # 64 experts, top-8: T = 2 and 24 on the 128-row kernel, 130 on the
+    # prefill tiles (16 rows per expert).
     d = SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=50 + T, T=T)
     x = synth.make_x_dev(T, d, seed=50 + T)
@@ -61,8 +63,8 @@ def test_grouped_small(hf, T):
 
 
 def test_grouped_small_prefill_tiles(hf):
-    # 96+ rows per expert on average: the grouped GEMMs switch to 192-row prefill
-    # tiles (experts with more rows take several).
+    # 4+ rows per expert on average: the grouped GEMMs switch to the prefill
+    # tiles (experts with more rows than a tile take several).
     T, d = 1024, SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=58, T=T)
     x = synth.make_x_dev(T, d, seed=58)
@@ -109,9 +111,9 @@ def test_prefill_tiles_fp32_activations(hf):
     r.free()
 
 
-@pytest.mark.parametrize("T", [767, 768])
+@pytest.mark.parametrize("T", [31, 32])
 def test_tile_size_switch_boundary(hf, T):
-    # 64 experts, top-8: T*k >= 96*E switches to 192-row tiles at T = 768.
+    # 64 experts, top-8: T*k >= 4*E switches to the prefill tiles at T = 32.
     d = SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=90 + T % 2, T=T)
     x = synth.make_x_dev(T, d, seed=90 + T % 2)
@@ -119,7 +121,7 @@ def test_tile_size_switch_boundary(hf, T):
     xh = x.download(np.float32, T * d).reshape(T, d)
     check_dispatch(res, SMALL["n_experts"])
     check_selection(r, res, T)
-    for t in range(0, T, 97):
+    for t in range(0, T, 7):
         r.check_token(xh[t], res, t)
     x.free()
     r.free()
@@ -159,7 +161,7 @@ def test_prefill_tiles_edge_shapes(hf, monkeypatch, name, dims, n_group, topk_gr
     res = r.forward(x, T)
     xh = x.download(np.float32, T * dims["hidden"]).reshape(T, -1)
     counts = check_dispatch(res, dims["n_experts"])
-    assert T * dims["top_k"] >= 96 * dims["n_experts"]  # the 192-row tile path
+    assert T * dims["top_k"] >= 4 * dims["n_experts"]  # the prefill tile path
     if dims["top_k"] == 1:
         assert counts.max() > 192  # experts over several tiles
     for t in range(0, T, 41):
@@ -232,8 +234,9 @@ def test_grouped_full_shape_batch_invariance(hf):
 
 
 def test_grouped_full_shape_t2560(hf):
-    # 2560 tokens: 128-row tiles still, and the router GEMM splits K 12 ways
-    # (its reduction takes partials eight at a time, then the rest).
+    # 2560 tokens (80 rows per expert: the prefill tiles), and the router
+    # GEMM splits K 12 ways (its reduction takes partials eight at a time,
+    # then the rest).
     T, d = 2560, FULL["hidden"]
     r = Run(FULL, n_group=8, topk_group=4, seed=68, T=T)
     x = synth.make_x_dev(T, d, seed=68)
@@ -250,16 +253,24 @@ def test_grouped_full_shape_t2560(hf):
 
 
 def test_grouped_repeat_is_deterministic(hf):
+    # T = 37 (prefill tiles, items drawn from counters) repeats bit for bit; a
+    # smaller batch (T = 5, the 128-row kernel) gives the same bits before and
+    # after it through the same workspace, and the larger batch's first rows
+    # within the tolerance (the two kernels order h's hi and lo products
+    # differently).
     T, d = 37, SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=67, T=T)
     x = synth.make_x_dev(T, d, seed=67)
+    c0 = r.forward(x, 5)
     a = r.forward(x, T)
     b = r.forward(x, T)
     for key in ("out", "logits", "idx", "w", "offsets", "perm"):
         assert np.array_equal(a[key].view(np.uint32), b[key].view(np.uint32)), key
-    # A smaller batch after a larger one reuses the same workspace.
     c = r.forward(x, 5)
-    assert np.array_equal(c["out"], a["out"][:5])
+    assert np.array_equal(c["out"].view(np.uint32), c0["out"].view(np.uint32))
+    assert np.array_equal(c["idx"], a["idx"][:5])
+    for t in range(5):
+        assert_close(c["out"][t], a["out"][t], f"token {t}: T = 5 against T = 37")
     x.free()
     r.free()
 

@@ -132,11 +132,11 @@ def layer_weights(dev, **override):
     return capi.LayerWeights(f["router"], f["bias"], f["sg"], f["su"], f["sd"], f["experts"], f["norm"], f["loc"], 0)
 
 
-@pytest.mark.parametrize("T", [1, 37, 1024])
+@pytest.mark.parametrize("T", [1, 24, 1024])
 def test_bf16_activations_match_fp32(hf, T):
     # hfmoe_moe_forward_bf16 takes x as BF16 bits and must give exactly what
     # hfmoe_moe_forward gives for the same values held as FP32: decode (T = 1),
-    # batched tiles (T = 37) and prefill tiles (T = 1024 over 64 experts).
+    # batched tiles (T = 24) and prefill tiles (T = 1024 over 64 experts).
     d = SMALL["hidden"]
     r = Run(SMALL, n_group=8, topk_group=4, seed=95, T=T)
     x = synth.make_x_dev(T, d, seed=95)

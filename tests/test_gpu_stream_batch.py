@@ -59,10 +59,10 @@ def counters():
 
 
 @pytest.mark.parametrize("dims,T,distinct,check_every", [
-    (SMALL, 37, None, 1),        # ~60 distinct experts over a 16-slot pool: waves of 8
+    (SMALL, 24, None, 1),        # ~60 distinct experts over a 16-slot pool: waves of 8 (128-row tiles)
     (SMALL, 1024, None, 64),     # prefill tiles (192 rows) with per-XCD work counters, cleared per wave
     (FULL, 64, 32, 8),           # full shape, 75.5 MB slots, ~130 distinct experts in waves of 8
-], ids=["small_t37", "small_t1024_prefill_tiles", "full_t64"])
+], ids=["small_t24", "small_t1024_prefill_tiles", "full_t64"])
 def test_streamed_batch(hf, dims, T, distinct, check_every):
     seed = 300 + T
     shape = synth.LayerShape(n_group=8, topk_group=4, **dims)
