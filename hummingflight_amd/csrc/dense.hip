@@ -111,9 +111,12 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
         return HFMOE_OK;
     }
     GroupedWorkspace& gw = g.gws;
-    // From 192 tokens on, the prefill tiles (measured faster than 128-row
-    // tiles at every T from 256 to 1024).
-    const int TR = T >= 192 ? kDenseTileRows : kGemmTileRows;
+    // Past one 128-row M tile, the 256-row tiles (HFMOE_DENSE_MIN_TOKENS): a
+    // second 128-row M tile streams all the weights again (at 6144 x 12288:
+    // T = 129 0.320 against 0.206 ms, 191 0.325 against 0.246), and the
+    // 256-row tiles were faster at every T from 256 to 1024; up to 128 tokens
+    // the 128-row kernel is (T = 128: 0.188 against 0.201 ms).
+    const int TR = T >= env_int("HFMOE_DENSE_MIN_TOKENS", kGemmTileRows + 1) ? kDenseTileRows : kGemmTileRows;
     const int I = L.dense_inter;
     prof_begin(p, "split_x", s);
     HF_CHECK_LAUNCH(launch_split_bf16(x, gw.xh, gw.xl, (size_t)T * c.d, gw.lo_flag, s), "split x");

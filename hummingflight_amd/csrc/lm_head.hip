@@ -212,7 +212,11 @@ static int lm_head_forward(const float* h, int T, float* logits, int* token, hip
     GroupedWorkspace& gw = g.gws;
     prof_begin(p, "split_x", s);
     HF_CHECK_LAUNCH(launch_split_bf16(xn, gw.xh, gw.xl, (size_t)T * c.d, gw.lo_flag, s), "split x");
-    const int TR = T >= 192 ? kDenseTileRows : kGemmTileRows;
+    // Past one 128-row M tile, the 256-row tiles (HFMOE_LM_MIN_TOKENS): a
+    // second 128-row M tile streams the whole table again (GLM vocab:
+    // T = 129-191 1.53-1.56 ms against 0.89-1.03 on one 256-row tile; up to
+    // 128 tokens the two are even, 0.77-0.88 ms).
+    const int TR = T >= env_int("HFMOE_LM_MIN_TOKENS", kGemmTileRows + 1) ? kDenseTileRows : kGemmTileRows;
     GemmArgs a{};
     a.K = c.d;
     a.N = L.vocab;

@@ -135,11 +135,12 @@ def test_dense_down_k_splits(hf, H, I, T):
     L.free()
 
 
-@pytest.mark.parametrize("T", [64, 191])
+@pytest.mark.parametrize("T", [64, 128, 191])
 def test_dense_glm_shape_small_batch_k_splits(hf, T):
-    # T < 192: 128-row tiles, the down projection's 48 items (96 at T = 191)
-    # split along K into partials summed in split order; every output against
-    # the float32 reference, two tokens against the oracle.
+    # T <= 128: one 128-row tile, the down projection's 48 items; T = 191: one
+    # 256-row tile, 24 items; split along K into partials summed in split
+    # order.  Every output against the float32 reference, two tokens against
+    # the oracle.
     H, I = 6144, 12288
     configure(H, 2048, 256, T)
     L = Dense(H, I, seed=41)

@@ -64,7 +64,7 @@ def check(head, h, logits, tokens, rows):
         assert got == int(np.argmax(logits[t]))
 
 
-@pytest.mark.parametrize("T", [1, 5, 300])
+@pytest.mark.parametrize("T", [1, 5, 150, 300])
 def test_lm_head_small(hf, T):
     H, V = 1024, 5003
     configure(H, 300)
