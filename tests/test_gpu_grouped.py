@@ -413,3 +413,36 @@ def test_prefill_down_weight_outside_fp16_range(hf):
     assert np.max(np.abs(res["out"][on_hot, row])) > 100.0  # the planted weight's share is there
     x.free()
     r.free()
+
+
+def test_two_tokens_take_the_decode_kernels(hf, monkeypatch):
+    # A plain call with T = 2 runs the two tokens through the decode kernels
+    # one at a time: bit-identical to two T = 1 calls, each token the
+    # oracle's; the grouped path (HFMOE_TOKENWISE_MAX_T=1, or any debug call)
+    # agrees within the tolerance.
+    T, d = 2, FULL["hidden"]
+    r = Run(FULL, n_group=8, topk_group=4, seed=72, T=T)
+    x = synth.make_x_dev(T, d, seed=72)
+    fwd = capi.load().hfmoe_moe_forward
+    both = capi.DeviceBuffer(T * d * 4)
+    one = capi.DeviceBuffer(T * d * 4)
+    capi.check(fwd(0, x.ptr, T, both.ptr, None))
+    for t in range(T):
+        capi.check(fwd(0, DevView(x, t * d * 4).ptr, 1, DevView(one, t * d * 4).ptr, None))
+    capi.call("hfmoe_synchronize")
+    got = both.download(np.float32, T * d).reshape(T, d)
+    assert np.array_equal(got.view(np.uint32), one.download(np.float32, T * d).reshape(T, d).view(np.uint32))
+    res = r.forward(x, T)  # debug call: the grouped path, its routing reported
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    for t in range(T):
+        ridx, ref = r.check_token(xh[t], res, t)
+        assert_close(got[t], ref, f"token {t}: decode kernels against the oracle")
+        assert_close(got[t], res["out"][t], f"token {t}: decode kernels against the grouped path")
+    monkeypatch.setenv("HFMOE_TOKENWISE_MAX_T", "1")
+    capi.check(fwd(0, x.ptr, T, both.ptr, None))
+    capi.call("hfmoe_synchronize")
+    monkeypatch.delenv("HFMOE_TOKENWISE_MAX_T")
+    assert np.array_equal(both.download(np.float32, T * d).reshape(T, d).view(np.uint32), res["out"].view(np.uint32))
+    for b in (x, both, one):
+        b.free()
+    r.free()
