@@ -1,14 +1,21 @@
-"""A full-shape prefill chunk of 6000 tokens (d = 6144, 256 experts top-8 + 1
-shared, near-uniform routing): ~187 rows per expert, so most experts span two
-M tiles of the 160-row tile list (the down projection's, and gate/up's with
-FP32 activations) and many two of the 192-row list (gate/up's with
-BF16-valued activations), and the shared expert's 6000 rows take 38 and 32
-tiles.  With BF16-valued and with FP32 activations:
+"""Full-shape prefill chunks larger than 4096 tokens (d = 6144, 256 experts
+top-8 + 1 shared, near-uniform routing):
+
+  * T = 6000: ~187 rows per expert, so most experts span two M tiles of the
+    160-row tile list (the down projection's, and gate/up's with FP32
+    activations) and many two of the 192-row list (gate/up's with BF16-valued
+    activations); the shared expert's 6000 rows take 38 and 32 tiles;
+  * T = 8192, the largest batch a configuration accepts (max_tokens): ~256
+    rows per expert, nearly every expert over two tiles of both lists, the
+    shared expert's rows in 52 and 43 tiles, 73,728 rows of h and y (the
+    largest workspace of this layer shape).
+
+With BF16-valued and with FP32 activations:
   * dispatch and every token's selection and routing weights bit-exact with
     the oracle's given the GPU's router logits;
-  * every one of the 36.9 M outputs against a float32 reference of the whole
-    layer (the oracle's weights and routing), as a share of the 1e-2
-    relative + 2e-3 absolute tolerance (must stay below 0.8);
+  * every output against a float32 reference of the whole layer (the
+    oracle's weights and routing), as a share of the 1e-2 relative + 2e-3
+    absolute tolerance (must stay below 0.8);
   * a token of every M tile of both tile lists against the oracle's moeLayer
     restatement;
   * bit for bit against the narrower split tiles (HFMOE_PREFILL_WIDE=0).
@@ -23,28 +30,31 @@ from moe_harness import (FULL, DeviceBackedLayer, Run, assert_close, layer_refer
 
 pytestmark = pytest.mark.gpu
 
-T, D, E, K = 6000, FULL["hidden"], FULL["n_experts"], FULL["top_k"]
-SEED = 67
+D, E, K = FULL["hidden"], FULL["n_experts"], FULL["top_k"]
+SEEDS = {6000: 67, 8192: 68}  # batch size -> seed of the layer and its tokens
 
 
-@pytest.fixture(scope="module")
-def layer67(hf):
-    bias = O.fill_f32(E, SEED, O.tensor_id(0, O.ROLE_BIAS), 0.0, 0.001)
-    r = Run(FULL, n_group=8, topk_group=4, seed=SEED, T=T, bias=bias)
+@pytest.fixture(scope="module", params=sorted(SEEDS), ids=lambda t: f"T{t}")
+def big_layer(request, hf):
+    T = request.param
+    seed = SEEDS[T]
+    print(f"T = {T}: building the full-shape layer (seed {seed})", flush=True)
+    bias = O.fill_f32(E, seed, O.tensor_id(0, O.ROLE_BIAS), 0.0, 0.001)
+    r = Run(FULL, n_group=8, topk_group=4, seed=seed, T=T, bias=bias)
     host = DeviceBackedLayer(r.spec, r.dev)
-    yield r, host
+    yield T, seed, r, host
     r.free()
 
 
 @pytest.mark.parametrize("fp32_x", [False, True], ids=["bf16_valued_x", "fp32_x"])
-def test_prefill_6000_two_tile_experts(layer67, fp32_x, monkeypatch):
-    r, host = layer67
-    xh = O.make_x(T, D, SEED).astype(np.float32)
+def test_prefill_large_multi_tile_experts(big_layer, fp32_x, monkeypatch):
+    T, seed, r, host = big_layer
+    xh = O.make_x(T, D, seed).astype(np.float32)
     if fp32_x:  # not BF16-valued: the x lo half enters the gate/up GEMM too
-        rng = np.random.default_rng(SEED)
+        rng = np.random.default_rng(seed)
         xh = (xh * (1.0 + np.float32(2.0 ** -10) * rng.standard_normal(xh.shape).astype(np.float32))).astype(
             np.float32)
-    what = "T = 6000, " + ("FP32 x" if fp32_x else "BF16-valued x")
+    what = f"T = {T}, " + ("FP32 x" if fp32_x else "BF16-valued x")
     print(f"{what}: forward", flush=True)
     x = capi.DeviceBuffer.of(xh)
     res = r.forward(x, T)
