@@ -2,14 +2,16 @@
 //
 // out = Wd . (silu(Wg . x) * (Wu . x)) with the dense intermediate size
 // (intermediateSize, config.h:16; 12288 at GLM-5.2 against 2048 per routed
-// expert).  No new kernels: the matrices are the same [out, in] BF16 layout as
-// an expert's, so
+// expert).  The matrices are the same [out, in] BF16 layout as an expert's,
+// so
 //   T = 1:  the decode GEMVs multiply them as a "shared expert" of
 //           inter / slice slices (the down GEMV sums the slices' partial
 //           products in a fixed order), no routed slots;
 //   T > 1:  the grouped GEMM multiplies every token row by the one weight set
 //           (one group, no dispatch): gate/up with the SwiGLU epilogue into
-//           h (BF16 hi + lo), then down straight into out.  h stays exact to
+//           h (BF16 hi + lo) -- for a short prompt split over K into FP32
+//           gate / up partials, the SwiGLU then applied to their sums by a
+//           small kernel -- then down straight into out.  h stays exact to
 //           ~16 bits, as in the MoE layer: the dense down projection sums
 //           12288 terms with weight 1, and an FP16 h moves its outputs by up
 //           to ~4e-3 at hidden 6144, past the 2e-3 absolute tolerance.
@@ -20,10 +22,21 @@ namespace hf {
 
 void dense_workspace_free() {
     DenseWorkspace& w = g.dws;
-    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl, (void*)w.part})
+    for (void* p : {(void*)w.h1, (void*)w.hh, (void*)w.hl, (void*)w.part, (void*)w.gu_part})
         if (p) hipFree(p);
     w = DenseWorkspace{};
 }
+
+// K splits of a short prompt's gate/up GEMM on the 256-row tiles (FP32 gate
+// and up partials, then the SwiGLU in swiglu_splits_kernel).  One M tile has
+// only 2 I / 256 items (96 at GLM-5.2's 12288) for 256 workgroups; two
+// splits measured at 6144 x 12288 (two boxes): T = 256 0.283-0.293 ->
+// 0.234-0.246 ms, 192 0.241 -> 0.209, 160 0.221 -> 0.190, 128 0.180-0.188 ->
+// 0.175-0.181, 64 0.130-0.140 -> 0.128-0.130 (the 128-row kernel unsplit
+// before); at T <= 32 even or slower (-3 % to +8 % by box), from two M tiles
+// (T = 384, 512) 6-7 % slower; three, four or eight splits slower than two
+// (288 / 384 / 768 items take two or three rounds of 256 workgroups).
+static int dense_gu_ksplit_auto(int T) { return T >= 64 && T <= kDenseTileRows ? 2 : 1; }
 
 static int dense_workspace_reserve(int inter) {
     DenseWorkspace& w = g.dws;
@@ -37,6 +50,10 @@ static int dense_workspace_reserve(int inter) {
     // down projection 24 items), 2 of a long one.
     const int part_rows = std::max(2 * tokens, std::min(8 * tokens, 4096));
     if (e == hipSuccess && tokens) e = hipMalloc(&w.part, sizeof(float) * (size_t)part_rows * g.cfg.d);
+    int gu_part_rows = 0;
+    for (int t = 2; t <= tokens; ++t) gu_part_rows = std::max(gu_part_rows, t * dense_gu_ksplit_auto(t));
+    if (e == hipSuccess && gu_part_rows > 0)
+        e = hipMalloc(&w.gu_part, sizeof(float) * (size_t)gu_part_rows * 2 * inter);
     if (e != hipSuccess) {
         dense_workspace_free();
         return fail(HFMOE_ERR_OUT_OF_MEMORY, "dense MLP workspace (inter %d, %d tokens): %s", inter, tokens,
@@ -45,7 +62,21 @@ static int dense_workspace_reserve(int inter) {
     w.inter = inter;
     w.tokens = tokens;
     w.part_rows = tokens ? part_rows : 0;
+    w.gu_part_rows = gu_part_rows;
     return HFMOE_OK;
+}
+
+// HFMOE_DENSE_GU_KSPLIT (1..8) overrides the choice; either only within the
+// partials' workspace (sized for the automatic choice at every T up to
+// max_tokens), with whole 64-wide K stages per split and tiles that do not
+// straddle the gate / up boundary.
+static int dense_gu_ksplit(int T, int I, int stages) {
+    const DenseWorkspace& w = g.dws;
+    const int want = env_int("HFMOE_DENSE_GU_KSPLIT", dense_gu_ksplit_auto(T));
+    if (want <= 1 || want > 8 || (size_t)want * T > (size_t)w.gu_part_rows || stages % want ||
+        I % gemm_tile_cols(kDenseTileRows, EPI_PARTIAL))
+        return 1;
+    return want;
 }
 
 // Slice rows for the decode kernels: the routed expert size when it divides
@@ -147,8 +178,28 @@ int dense_forward(LayerState& L, const float* x, int T, float* out, hipStream_t 
     // at T = 150 and 191 took gate/up 169-172 us like contiguous ranges.)
     const int by_ntile = TR == kDenseTileRows && env_int("HFMOE_DENSE_BY_NTILE", 1) != 0 ? 4 : 0;
     gu.by_ntile = by_ntile;
-    prof_begin(p, "dense_gateup_gemm", s);
-    HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "dense gate/up gemm");
+    const int gu_ks = dense_gu_ksplit(T, I, c.d / kGemmTileK);
+    if (gu_ks > 1) {
+        // Gate and up as one [2 I, d] matrix (b_split) on 256-row tiles,
+        // FP32 partials per K split, then silu(g) * u and the h split from
+        // their sums.
+        gu.tile_rows = kDenseTileRows;
+        gu.m_tiles = (T + kDenseTileRows - 1) / kDenseTileRows;
+        gu.by_ntile = env_int("HFMOE_DENSE_BY_NTILE", 1) != 0 ? 4 : 0;
+        gu.N = 2 * I;
+        gu.tile_cols = gemm_tile_cols(kDenseTileRows, EPI_PARTIAL);
+        gu.n_tiles = gemm_n_tiles(EPI_PARTIAL, 2 * I, gu.tile_cols);
+        gu.b_split = I;
+        gu.out_f32 = w.gu_part;
+        gu.ksplit = gu_ks;
+        prof_begin(p, "dense_gateup_gemm", s);
+        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_PARTIAL, gu, gemm_blocks(kDenseTileRows), s), "dense gate/up gemm");
+        prof_begin(p, "dense_swiglu", s);
+        HF_CHECK_LAUNCH(launch_swiglu_splits(w.gu_part, gu_ks, T, I, w.hh, w.hl, s), "dense gate/up split sum");
+    } else {
+        prof_begin(p, "dense_gateup_gemm", s);
+        HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SWIGLU, gu, gemm_blocks(TR), s), "dense gate/up gemm");
+    }
     GemmArgs dn{};
     dn.K = I;
     dn.N = c.d;

@@ -167,7 +167,7 @@ int grouped_route(LayerState& L, const float* x, int T, hipStream_t s) {
     prof_begin(p, "dispatch", s);
     TileList tl{TR, w.tile_expert, w.tile_row0, w.ntiles}, tl_gu{};
     w.wide = prefill_wide(TR);
-    if (w.wide) tl_gu = TileList{kWideTileRows, w.tile_expert_gu, w.tile_row0_gu, w.ntiles + 32};
+    if (w.wide) tl_gu = TileList{kWideTileRows, w.tile_expert_gu, w.tile_row0_gu, w.ntiles_wide()};
     HF_CHECK_LAUNCH(launch_dispatch(g.ws.idx, T, c.k, c.E, tl, tl_gu, shared_rows, w.counts, w.offsets, w.perm,
                                     w.row_token, w.chunk_hist, TR == kPrefillTileRows ? w.item_ctr : nullptr, s),
                     "dispatch");
@@ -198,7 +198,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     if (wide) {  // x with a lo half: the 160-row tiles
         gu.lo_tiles.group = w.tile_expert_gu;
         gu.lo_tiles.row0 = w.tile_row0_gu;
-        gu.lo_tiles.count = w.ntiles + 32;
+        gu.lo_tiles.count = w.ntiles_wide();
         gu.lo_tiles.shared_mtiles = (shared_rows + kWideTileRows - 1) / kWideTileRows;
     }
     gu.group_end = w.offsets + 1;
@@ -237,7 +237,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.n_tiles = gemm_n_tiles(EPI_SCATTER, c.d, dn.tile_cols);
     dn.tile_group = dn_wide ? w.tile_expert_gu : w.tile_expert;
     dn.tile_row0 = dn_wide ? w.tile_row0_gu : w.tile_row0;
-    dn.ntiles_dev = dn_wide ? w.ntiles + 32 : w.ntiles;
+    dn.ntiles_dev = dn_wide ? w.ntiles_wide() : w.ntiles;
     dn.group_end = w.offsets + 1;
     dn.rows_total = P + shared_rows;
     dn.a_hi = w.hh;

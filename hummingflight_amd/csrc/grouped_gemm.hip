@@ -239,20 +239,22 @@ __device__ __forceinline__ ItemRange item_range(const GemmArgs& a, int m_tiles) 
 // of 4 whenever N is a multiple of 64; a ragged router width falls back to
 // single floats) to output row orow_idx (SCATTER: the token-order row of gr;
 // PARTIAL: gr).  NT: non-temporal stores.
+// h = silu(g) * u with the hardware exp2 and reciprocal (a few ulp of FP32):
+// far below the rounding of h to a BF16 hi + lo pair.  The one formula of the
+// GEMM epilogue and of the split-K SwiGLU kernel.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 template <int EPI, int NCB, bool NT = false>
 __device__ __forceinline__ void store_tile_row(const GemmArgs& a, const f32x4_t (&acc)[NCB], int gr, int col0,
                                                int ks, int orow_idx) {
     if (EPI == EPI_SWIGLU) {
-        // h = silu(g) * u with the hardware exp2 and reciprocal (a few ulp of
-        // FP32): far below the rounding of h to a BF16 hi + lo pair.
         float hv[NCB / 2][4];
 #pragma unroll
         for (int cb = 0; cb < NCB / 2; ++cb)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float gv = acc[cb][q];
-                hv[cb][q] = gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * acc[cb + NCB / 2][q];
-            }
+            for (int q = 0; q < 4; ++q) hv[cb][q] = silu_mul(acc[cb][q], acc[cb + NCB / 2][q]);
         {  // BF16 hi + lo halves
             uint16_t* hrow = a.h_hi + (size_t)gr * a.N;
             uint16_t* lrow = a.h_lo + (size_t)gr * a.N;
@@ -654,9 +656,13 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         n = min(n, a.N - 1);
         boff[j] = (uint32_t)(2 * ((size_t)n * a.b_ld + kbase + c * 8));
     }
+    // A PARTIAL tile past b_split lies wholly in the second matrix: its rows
+    // n address b_fixed1 from a base b_split rows before it.
+    const uint16_t* bsel = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
+    if (EPI == EPI_PARTIAL && a.b_split > 0 && n0 >= a.b_split) bsel = b1 - (size_t)a.b_split * a.b_ld;
     // Byte offsets within 4 GiB of each operand's base (every activation and
     // weight buffer of a layer is far smaller).
-    const __amdgpu_buffer_rsrc_t rb = raw_rsrc(uniform_ptr((EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0));
+    const __amdgpu_buffer_rsrc_t rb = raw_rsrc(uniform_ptr(bsel));
     const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(a.a_hi);
     const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
 
@@ -1371,6 +1377,57 @@ hipError_t launch_sum_splits(const float* part, int ks, size_t n, float* out, hi
     return launch(sum_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, ks, n4, out);
 }
 
+// Four consecutive h columns of one token per thread: g and u summed over the
+// splits in split order (as sum_splits_kernel sums), then the epilogue's
+// silu_mul and hi / lo split.
+__global__ void swiglu_splits_kernel(const float* __restrict__ part, int ks, int T, int I,
+                                     uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo) {
+    const int i4 = I >> 2;
+    const size_t n4 = (size_t)T * i4;
+    const size_t split4 = (size_t)T * (I >> 1);  // f32x4 elements per split: [T][2 I]
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(part);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const size_t t = i / i4, c4 = i % i4;
+        const size_t gi = t * 2 * i4 + c4;  // gate columns 4 c4.., up columns I + 4 c4..
+        f32x4_t gv = __builtin_nontemporal_load(p4 + gi);
+        f32x4_t uv = __builtin_nontemporal_load(p4 + gi + i4);
+        for (int k = 1; k < ks; ++k) {
+            gv += __builtin_nontemporal_load(p4 + k * split4 + gi);
+            uv += __builtin_nontemporal_load(p4 + k * split4 + gi + i4);
+        }
+        uint32_t hw[2], lw[2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float h = silu_mul(gv[q], uv[q]);
+            const uint32_t v0 = f32_to_bf16(h);
+            const uint32_t v1 = f32_to_bf16(h - __uint_as_float(v0 << 16));
+            if (q & 1) {
+                hw[q >> 1] |= v0 << 16;
+                lw[q >> 1] |= v1 << 16;
+            } else {
+                hw[q >> 1] = v0;
+                lw[q >> 1] = v1;
+            }
+        }
+        reinterpret_cast<uint2*>(h_hi)[i] = make_uint2(hw[0], hw[1]);
+        reinterpret_cast<uint2*>(h_lo)[i] = make_uint2(lw[0], lw[1]);
+    }
+}
+
+hipError_t launch_swiglu_splits(const float* part, int ks, int T, int I, uint16_t* h_hi, uint16_t* h_lo,
+                                hipStream_t s) {
+    if (ks < 1 || T < 0 || I <= 0 || I % 4 ||
+        ((reinterpret_cast<uintptr_t>(part) & 15) | (reinterpret_cast<uintptr_t>(h_hi) & 7) |
+         (reinterpret_cast<uintptr_t>(h_lo) & 7)))
+        return hipErrorInvalidValue;
+    const size_t n4 = (size_t)T * (I / 4);
+    size_t blocks = (n4 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks == 0) return hipSuccess;
+    return launch(swiglu_splits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, ks, T, I, h_hi, h_lo);
+}
+
 __global__ void clear_u32_kernel(unsigned* p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0u;
@@ -1483,6 +1540,12 @@ hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream
     const size_t lim = (size_t)1 << 32;
     if (a.tile_rows != kGemmTileRows &&
         ((size_t)a.N * (size_t)a.b_ld * 2 >= lim || (size_t)a.rows_total * (size_t)a.K * 2 >= lim))
+        return hipErrorInvalidValue;
+    // A second fixed matrix along N: split-kernel PARTIAL tiles that stay on
+    // one side of the boundary.
+    if (a.b_split && (epi != EPI_PARTIAL || a.b_tab || !a.b_fixed1 || a.b_split < 0 || a.b_split >= a.N ||
+                      (a.tile_rows != kPrefillTileRows && a.tile_rows != kDenseTileRows) ||
+                      a.b_split % a.tile_cols))
         return hipErrorInvalidValue;
     switch (epi) {
         case EPI_PARTIAL: return launch_epi<EPI_PARTIAL>(a, blocks, s);

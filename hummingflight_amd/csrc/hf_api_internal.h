@@ -38,7 +38,9 @@ struct GroupedWorkspace {
     int* row_token = nullptr;    // [rows] token of each sorted row
     int* tile_expert = nullptr;  // [max_tiles] group of each M tile
     int* tile_row0 = nullptr;    // [max_tiles] first sorted row of each M tile
-    int* ntiles = nullptr;       // [64] M tiles in use: [0] this list, [32] the wide gate/up list
+    int* ntiles = nullptr;       // [64] M tiles in use: [0] this list, [kWideCountAt] the wide list
+    static constexpr int kWideCountAt = 32;  // its own 128-byte line
+    int* ntiles_wide() const { return ntiles + kWideCountAt; }
     int* tile_expert_gu = nullptr;  // [max_tiles] the wide kernel's tiles (kWideTileRows rows)
     int* tile_row0_gu = nullptr;
     bool wide = false;              // the last dispatch wrote that list (the GEMMs after it take the wide tiles)
@@ -83,9 +85,11 @@ struct DenseWorkspace {
     uint16_t* hh = nullptr;  // [max_tokens, inter] h hi (multi-token path)
     uint16_t* hl = nullptr;  // [max_tokens, inter] h lo
     float* part = nullptr;   // [part_rows, hidden] K-split partials of the down projection
+    float* gu_part = nullptr;  // [gu_part_rows, 2 inter] K-split gate / up partials
     int inter = 0;
     int tokens = 0;
     int part_rows = 0;       // max(2 * max_tokens, min(8 * max_tokens, 4096))
+    int gu_part_rows = 0;    // splits x tokens the gate/up partials hold
 };
 
 struct Pending {

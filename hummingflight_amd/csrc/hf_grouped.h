@@ -61,6 +61,12 @@ struct GemmArgs {
     const uint16_t* b_fixed0;
     const uint16_t* b_fixed1;
     int b_ld;                   // B row stride in elements
+    // PARTIAL with fixed B on the split kernel's tiles (tile_rows
+    // kPrefillTileRows or kDenseTileRows): output columns [b_split, N)
+    // multiply rows (column - b_split) of b_fixed1, the columns before them
+    // b_fixed0's (a gate / up pair as one [2 I, K] matrix; b_split a multiple
+    // of the tile's columns).  0: b_fixed0 only.
+    int b_split;
     // epilogue operands
     float* out_f32;             // PARTIAL [ksplit][rows][N]; SCATTER y rows
     uint16_t* h_hi;             // SWIGLU h [rows][N] hi / lo
@@ -99,6 +105,12 @@ hipError_t launch_grouped_gemm(int epi, const GemmArgs& a, int blocks, hipStream
 hipError_t launch_clear_u32(unsigned* p, int n, hipStream_t s);
 // out[i] = sum over k < ks of part[k * n + i], in k order (n a multiple of 4).
 hipError_t launch_sum_splits(const float* part, int ks, size_t n, float* out, hipStream_t s);
+// The SWIGLU epilogue after a gate/up GEMM split over K: part is
+// [ks][T][2 I] FP32 (gate columns [0, I), up [I, 2 I)); g and u are the sums
+// over the splits in split order, h = silu(g) * u goes out as BF16 hi / lo
+// [T][I] (I a multiple of 4).
+hipError_t launch_swiglu_splits(const float* part, int ks, int T, int I, uint16_t* h_hi, uint16_t* h_lo,
+                                hipStream_t s);
 hipError_t launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, size_t n, unsigned* flag,
                              hipStream_t s);
 // out[t] = sum_r wts[t, r] * y[t*k + r] (+ y[shared_row0 + t] when shared_row0 >= 0); d % 4 == 0.

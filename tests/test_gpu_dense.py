@@ -3,7 +3,7 @@
 The oracle's dense_mlp is pinned bit-exact to the reference's own denseMlp
 (tests/test_oracle.py).  Here the library's decode path (T = 1: the expert
 GEMVs over inter / slice slices) and multi-token path (one-group grouped GEMM,
-128- and 192-row tiles) must agree with it within 1e-2 relative + 2e-3
+128- and 256-row tiles, K splits) must agree with it within 1e-2 relative + 2e-3
 absolute, at a small shape and at GLM-5.2's (hidden 6144, intermediate 12288);
 the RMSNorm + residual block and a dense layer loaded from a checkpoint too.
 """
@@ -149,6 +149,32 @@ def test_dense_glm_shape_small_batch_k_splits(hf, T):
     for t in (0, T - 1):
         assert_close(y[t], L.ref(x[t]), f"T={T} token {t}")
     assert_close(y, ref_all(L, x), f"T={T} every output")
+    L.free()
+
+
+@pytest.mark.parametrize("T,ks", [(64, None), (160, 3), (128, 4), (64, 8)])
+def test_dense_gate_up_k_splits(hf, monkeypatch, T, ks):
+    # One 256-row M tile gives the gate/up GEMM 96 items: from 64 to 256
+    # tokens it splits K in two (None: the automatic choice), gate and up
+    # partials in FP32 summed in split order before the SwiGLU.  The split
+    # sums round differently from the unsplit GEMM's (so the outputs must
+    # differ: the split path ran), and both hold every output to the float32
+    # reference; a token of each against the oracle.
+    H, I = 6144, 12288
+    configure(H, 2048, 256, 512)  # partials for 2 splits x 256 tokens: room for 3 x 160, 4 x 128, 8 x 64
+    L = Dense(H, I, seed=43)
+    x = np.random.default_rng(43).standard_normal((T, H)).astype(np.float32)
+    if ks:
+        monkeypatch.setenv("HFMOE_DENSE_GU_KSPLIT", str(ks))
+    y = L.forward(x)
+    monkeypatch.setenv("HFMOE_DENSE_GU_KSPLIT", "1")
+    y1 = L.forward(x)
+    monkeypatch.delenv("HFMOE_DENSE_GU_KSPLIT")
+    assert not np.array_equal(y.view(np.uint32), y1.view(np.uint32)), "the split path did not run"
+    ref = ref_all(L, x)
+    assert_close(y, ref, f"T={T} split every output")
+    assert_close(y1, ref, f"T={T} unsplit every output")
+    assert_close(y[T - 1], L.ref(x[T - 1]), f"T={T} split token {T - 1}")
     L.free()
 
 
