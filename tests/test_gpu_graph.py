@@ -1,21 +1,24 @@
-"""The MoE forward captured into a HIP graph and replayed.
+"""The MoE forward and the dense MLP captured into a HIP graph and replayed.
 
 A serving loop may capture a layer (or a chain of layers) once and replay it.
-The forward issues only kernel launches on the caller's stream -- no memsets,
-no host synchronisation, no allocation -- so stream capture records it
+The forwards issue only kernel launches on the caller's stream -- no memsets,
+no host synchronisation, no allocation -- so stream capture records them
 whole.  Every replay is checked bit for bit against the same call made
-eagerly, with other eager work on the stream between replays, at T = 1
-(decode kernels), T = 24 (128-row grouped GEMM) and T = 1024 (192-row tiles,
-multi-workgroup dispatch, per-XCD work counters that the dispatch zeroes on
-every replay).
+eagerly, with other eager work on the stream between replays: the MoE layer
+at T = 1 (decode kernels), T = 24 (128-row grouped GEMM) and T = 1024
+(192-row tiles, multi-workgroup dispatch, per-XCD work counters that the
+dispatch zeroes on every replay); the dense MLP at T = 1 (GEMVs), T = 64
+(gate/up split over K, SwiGLU on the split sums, down in K splits) and
+T = 300 (256-row tiles dealt per XCD).
 """
 import ctypes as C
 
 import numpy as np
 import pytest
 
+import oracle as O
 from hummingflight_amd import capi, synth
-from moe_harness import SMALL, Run
+from moe_harness import SMALL, Run, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -145,3 +148,57 @@ def test_replays_follow_the_activation_type(hf):
         for b in (xin, out):
             b.free()
         r.free()
+
+
+@pytest.mark.parametrize("T", [1, 64, 300])
+def test_dense_forward_replays_from_hip_graph(hf, T):
+    H, I, seed = 1024, 3072, 90 + T % 7
+    shape = synth.LayerShape(hidden=H, inter=512, n_experts=64, top_k=8, n_group=8, topk_group=4)
+    capi.call("hfmoe_configure", shape.config(max_tokens=300))
+    w = [capi.DeviceBuffer(2 * H * I) for _ in range(3)]
+    for i, b in enumerate(w):
+        synth.fill_bf16(b.ptr, H * I, seed, 100 + i, 0.0, 0.02)
+    dw = capi.DenseWeights(w[0].ptr, w[1].ptr, w[2].ptr, None, I, 0)
+    capi.call("hfmoe_register_dense_layer", 0, C.byref(dw))
+    x = synth.make_x_dev(T, H, seed=seed)
+    x2 = synth.make_x_dev(T, H, seed=seed + 1)
+    out_e = capi.DeviceBuffer(T * H * 4)
+    out_g = capi.DeviceBuffer(T * H * 4)
+    fwd = capi.load().hfmoe_dense_mlp_forward
+    h = hip()
+    s = C.c_void_p()
+    ok(h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        capi.check(fwd(0, x.ptr, T, out_e.ptr, s))
+        ok(h.hipStreamSynchronize(s), "sync")
+        ref = out_e.download(np.float32, T * H).copy()
+
+        ok(h.hipStreamBeginCapture(s, CAPTURE_MODE_RELAXED), "hipStreamBeginCapture")
+        rc = fwd(0, x.ptr, T, out_g.ptr, s)
+        ok(h.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
+        capi.check(rc)
+        ok(h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+
+        for rep in range(4):
+            capi.call("hfmoe_memset", out_g.ptr, 0, T * H * 4)
+            ok(h.hipGraphLaunch(exe, s), "hipGraphLaunch")
+            ok(h.hipStreamSynchronize(s), "sync")
+            got = out_g.download(np.float32, T * H)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"replay {rep} differs from eager"
+            # Other work through the same workspace between replays.
+            capi.check(fwd(0, x2.ptr, T, out_e.ptr, s))
+            ok(h.hipStreamSynchronize(s), "sync")
+        assert not np.array_equal(out_e.download(np.float32, T * H), ref)
+        # The last token against the oracle's denseMlp restatement.
+        hw = [O.fill_bf16(H * I, seed, 100 + i, 0.0, 0.02) for i in range(3)]
+        xt = x.download(np.float32, T * H).reshape(T, H)[T - 1]
+        assert_close(ref.reshape(T, H)[T - 1], O.dense_mlp(hw[0], hw[1], hw[2], xt, H, I), f"T={T} last token")
+    finally:
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamDestroy(s)
+        for b in w + [x, x2, out_e, out_g]:
+            b.free()
