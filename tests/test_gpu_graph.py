@@ -9,7 +9,9 @@ at T = 1 (decode kernels), T = 24 (128-row grouped GEMM) and T = 1024
 (192-row tiles, multi-workgroup dispatch, per-XCD work counters that the
 dispatch zeroes on every replay); the dense MLP at T = 1 (GEMVs), T = 64
 (gate/up split over K, SwiGLU on the split sums, down in K splits) and
-T = 300 (256-row tiles dealt per XCD).
+T = 300 (256-row tiles dealt per XCD); the LM head's logits and greedy
+tokens at T = 1 (GEMV with the fused argmax and its merge launch), 5 and 150
+(grouped GEMM, then the row argmax).
 """
 import ctypes as C
 
@@ -201,4 +203,64 @@ def test_dense_forward_replays_from_hip_graph(hf, T):
             h.hipGraphDestroy(graph)
         h.hipStreamDestroy(s)
         for b in w + [x, x2, out_e, out_g]:
+            b.free()
+
+
+@pytest.mark.parametrize("T", [1, 5, 150])
+def test_lm_head_replays_from_hip_graph(hf, T):
+    H, V, seed = 1024, 5003, 95 + T % 7
+    shape = synth.LayerShape(hidden=H, inter=512, n_experts=64, top_k=8, n_group=8, topk_group=4)
+    capi.call("hfmoe_configure", shape.config(max_tokens=150))
+    Wd = capi.DeviceBuffer(2 * V * H)
+    synth.fill_bf16(Wd.ptr, V * H, seed, 300, 0.0, 0.02)
+    nd = capi.DeviceBuffer(2 * H)
+    synth.fill_bf16(nd.ptr, H, seed, 301, 1.0, 0.05)
+    capi.call("hfmoe_register_lm_head", Wd.ptr, nd.ptr, V)
+    x = synth.make_x_dev(T, H, seed=seed)
+    x2 = synth.make_x_dev(T, H, seed=seed + 1)
+    lg_e, lg_g = capi.DeviceBuffer(T * V * 4), capi.DeviceBuffer(T * V * 4)
+    tk_e, tk_g = capi.DeviceBuffer(T * 4), capi.DeviceBuffer(T * 4)
+    head = capi.load().hfmoe_lm_head
+    h = hip()
+    s = C.c_void_p()
+    ok(h.hipStreamCreate(C.byref(s)), "hipStreamCreate")
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        capi.check(head(x.ptr, T, lg_e.ptr, tk_e.ptr, s))
+        ok(h.hipStreamSynchronize(s), "sync")
+        ref_lg = lg_e.download(np.float32, T * V).copy()
+        ref_tk = tk_e.download(np.int32, T).copy()
+
+        ok(h.hipStreamBeginCapture(s, CAPTURE_MODE_RELAXED), "hipStreamBeginCapture")
+        rc = head(x.ptr, T, lg_g.ptr, tk_g.ptr, s)
+        ok(h.hipStreamEndCapture(s, C.byref(graph)), "hipStreamEndCapture")
+        capi.check(rc)
+        ok(h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+
+        for rep in range(4):
+            capi.call("hfmoe_memset", lg_g.ptr, 0, T * V * 4)
+            capi.call("hfmoe_memset", tk_g.ptr, 255, T * 4)
+            ok(h.hipGraphLaunch(exe, s), "hipGraphLaunch")
+            ok(h.hipStreamSynchronize(s), "sync")
+            got = lg_g.download(np.float32, T * V)
+            assert np.array_equal(got.view(np.uint32), ref_lg.view(np.uint32)), f"replay {rep}: logits differ"
+            assert np.array_equal(tk_g.download(np.int32, T), ref_tk), f"replay {rep}: tokens differ"
+            # Other work through the same workspace between replays.
+            capi.check(head(x2.ptr, T, lg_e.ptr, tk_e.ptr, s))
+            ok(h.hipStreamSynchronize(s), "sync")
+        assert not np.array_equal(lg_e.download(np.float32, T * V), ref_lg)
+        # The eager call's last token against the oracle's lmHeadAndSample restatement.
+        W = O.fill_bf16(V * H, seed, 300, 0.0, 0.02)
+        norm = O.fill_bf16(H, seed, 301, 1.0, 0.05)
+        xt = x.download(np.float32, T * H).reshape(T, H)[T - 1]
+        ref, _ = O.lm_head(W, norm, xt, V, 1e-5)
+        assert_close(ref_lg.reshape(T, V)[T - 1], ref, f"T={T} last token logits")
+        assert int(ref_tk[T - 1]) == int(np.argmax(ref_lg.reshape(T, V)[T - 1]))
+    finally:
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamDestroy(s)
+        for b in (Wd, nd, x, x2, lg_e, lg_g, tk_e, tk_g):
             b.free()
