@@ -249,7 +249,7 @@ int grouped_experts(const uint16_t* const* etab, int T, hipStream_t s) {
     dn.scatter_rows = w.perm;
     dn.ksplit = 1;
     dn.item_ctr = TR == kPrefillTileRows ? w.item_ctr + kItemCounters / 2 : nullptr;
-    dn.shared_mtiles = dn_wide ? gu.lo_tiles.shared_mtiles : gu.shared_mtiles;
+    dn.shared_mtiles = dn_wide ? (shared_rows + kWideTileRows - 1) / kWideTileRows : gu.shared_mtiles;
     prof_begin(p, "expert_down_gemm", s);
     HF_CHECK_LAUNCH(launch_grouped_gemm(EPI_SCATTER, dn, gemm_blocks(TR), s), "down gemm");
     return HFMOE_OK;
