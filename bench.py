@@ -897,7 +897,11 @@ def run_configs(args, cpu_tokens_per_s: float | None = None) -> dict:
             keep["cpu_baseline"] = {"value": round(cpu_tokens_per_s / layers, 2), "unit": "tokens/s",
                                     "kind": "reference",
                                     "sample": "the decode line's cpu_baseline per token"
-                                              + (f", over {layers} layers" if layers > 1 else "")}
+                                              + (f", over {layers} layers" if layers > 1 else "")
+                                              + ": the reference has no batched MoE; it calls moeLayer once per "
+                                                "token of a batch, each call reading 8 routed + 1 shared experts "
+                                                "of equal size, so its tokens/s at any batch size is its T = 1 "
+                                                "call rate"}
         out[name] = keep
         print(f"{name}: {keep['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
     return out
