@@ -866,8 +866,8 @@ METRICS = {
 
 
 def run_configs(args, cpu_tokens_per_s: float | None = None) -> dict:
-    """The north star's other configurations of the same full-shape layer,
-    timed in the default run beside the decode line: batched decode (T=64,
+    """The other benchmark workloads of the same full-shape layer, timed in
+    the default run beside the decode line: batched decode (T=64,
     Zipf popularity), prefill (T=4096, BF16-valued and FP32 activations) and
     the 8-layer streamed chain (T=1, experts from pinned host RAM).  Each
     with steps of its own; no CPU legs (the reference runs every batch token
