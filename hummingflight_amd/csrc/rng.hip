@@ -6,7 +6,7 @@
 // conversion and power-of-two scaling: mean 0, variance ~1, an Irwin-Hall(12)
 // approximation of N(0,1)); value = (z*std) + mean with two IEEE roundings and
 // no contraction.  Any host that evaluates the same integer steps gets the same
-// bits, so a CPU checker can regenerate any expert independently of the GPU.
+// bits, so the CPU oracle can regenerate any expert independently of the GPU.
 #include "hf_common.h"
 #include "hf_kernels.h"
 

@@ -1,4 +1,4 @@
-"""ctypes bindings for the CPU checker (test infrastructure only).
+"""ctypes bindings for the CPU oracle (test infrastructure only).
 
 `liboracle.so` is the C restatement of the reference MoE forward (oracle.c);
 `_ref/libhfref.so` is the reference's own code behind a thin harness, built only

@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of HummingFlight's MoE-block forward.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never part of it.
+ * TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against, never part of it.
  * Built by oracle/Makefile with gcc -O2 -ffp-contract=off (no -march): scalar,
  * serial FP32 accumulation with separate multiply and add, which is what the
  * reference's CMake build produces on Linux/GCC (CMakeLists.txt:62-77 adds no

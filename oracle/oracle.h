@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of HummingFlight's MoE-block forward.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP path
  * (hummingflight_amd/csrc) is compared against.  Only tests/, the smoke() entry
  * and the cpu_baseline leg of bench.py may load it; the product never links,
  * loads or calls it.

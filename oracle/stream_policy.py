@@ -1,6 +1,6 @@
 """CPU restatement of the streamed-expert cache and copy-ahead policy.
 
-Test infrastructure only (tests/ use it as the checker; the product never
+Test infrastructure only (tests/ use it as the oracle; the product never
 imports it).  It restates, per routing event of a streamed layer:
 
 * the HBM slot cache: a lookup of a resident (layer, expert) reuses its slot

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the HIP path is tested against it.
 
 Each function is checked against the reference's own outputs
 (tests/golden/reference_vectors.json, written by gen_golden.py from the
