@@ -30,10 +30,10 @@ void dense_workspace_free() {
 // K splits of a short prompt's gate/up GEMM on the 256-row tiles (FP32 gate
 // and up partials, then the SwiGLU in swiglu_splits_kernel).  One M tile has
 // only 2 I / 256 items (96 at GLM-5.2's 12288) for 256 workgroups; two
-// splits measured at 6144 x 12288 (two boxes): T = 256 0.283-0.293 ->
+// splits measured at 6144 x 12288 (two MI355X machines): T = 256 0.283-0.293 ->
 // 0.234-0.246 ms, 192 0.241 -> 0.209, 160 0.221 -> 0.190, 128 0.180-0.188 ->
 // 0.175-0.181, 64 0.130-0.140 -> 0.128-0.130 (the 128-row kernel unsplit
-// before); at T <= 32 even or slower (-3 % to +8 % by box), from two M tiles
+// before); at T <= 32 even or slower (-3 % to +8 % by machine), from two M tiles
 // (T = 384, 512) 6-7 % slower; three, four or eight splits slower than two
 // (288 / 384 / 768 items take two or three rounds of 256 workgroups).
 static int dense_gu_ksplit_auto(int T) { return T >= 64 && T <= kDenseTileRows ? 2 : 1; }
