@@ -469,8 +469,14 @@ int hfmoe_mlp_block(int layer, float* h_dev, int32_t T, void* stream) {
     if (rc) return rc;
     auto it = g.layers.find(layer);
     if (it == g.layers.end()) return fail(HFMOE_ERR_NOT_REGISTERED, "layer %d is not registered", layer);
-    if (T <= 0 || T > g.max_tokens)
-        return fail(HFMOE_ERR_INVALID_ARGUMENT, "T=%d outside 1..max_tokens=%d", T, g.max_tokens);
+    if (T < 0 || T > g.max_tokens)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "T=%d outside 0..max_tokens=%d", T, g.max_tokens);
+    if (T == 0) return HFMOE_OK;
+    // The RMSNorm reads and the residual add writes h in 16-byte vectors.
+    if (!h_dev) return fail(HFMOE_ERR_INVALID_ARGUMENT, "null hidden state pointer");
+    if (reinterpret_cast<uintptr_t>(h_dev) & 15)
+        return fail(HFMOE_ERR_INVALID_ARGUMENT, "hidden state must be 16-byte aligned");
+    if (!g.ws.tmp) return fail(HFMOE_ERR_NOT_INITIALIZED, "workspace is not allocated");
     hipStream_t s = pick_stream(stream);
     float* xn = g.ws.tmp;
     float* mo = g.ws.tmp + (size_t)T * g.cfg.d;

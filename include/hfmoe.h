@@ -133,7 +133,8 @@ int hfmoe_moe_forward_bf16(int layer, const uint16_t* x_dev, int32_t T, float* o
 int hfmoe_moe_layer(int layer, const float* input_host, float* output_host);
 /* h_dev[T, hidden] += MLP(RMSNorm(h_dev)) -- the MLP half of a decoder layer
  * (glm_forward.cpp:785-796): the MoE block, or the dense MLP for a layer
- * registered with hfmoe_register_dense_layer. */
+ * registered with hfmoe_register_dense_layer.  h_dev 16-byte aligned; T = 0
+ * does nothing. */
 int hfmoe_mlp_block(int layer, float* h_dev, int32_t T, void* stream);
 
 /* ---- dense MLP layers (the first first_k_dense_replace layers, config.h:53;

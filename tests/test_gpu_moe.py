@@ -335,3 +335,62 @@ def test_engine_shim_cpp_caller(hf):
         got = np.array([int(v, 16) for v in lines[t].split()], np.uint32).view(np.float32)
         out, _, _, _ = ref.forward(xs[t])
         assert_close(got, out, f"engine shim token {t}")
+
+
+def test_entry_points_reject_bad_arguments(hf):
+    # Every forward entry point checks its arguments before it launches
+    # anything: T past max_tokens or negative, null or misaligned buffers,
+    # a layer of the other kind, an unregistered layer; T = 0 does nothing.
+    # The library stays usable after every refusal.
+    L = capi.load()
+    T, d = 4, SMALL["hidden"]
+    r = Run(SMALL, seed=9, T=T)  # max_tokens = 4; MoE layer 0
+    I, V = 3 * SMALL["inter"], 1000
+    dense = [capi.DeviceBuffer(2 * d * I) for _ in range(3)]
+    for i, b in enumerate(dense):
+        synth.fill_bf16(b.ptr, d * I, 9, 100 + i, 0.0, 0.02)
+    capi.call("hfmoe_register_dense_layer", 1,
+              C.byref(capi.DenseWeights(dense[0].ptr, dense[1].ptr, dense[2].ptr, None, I, 0)))
+    head = capi.DeviceBuffer(2 * V * d)
+    synth.fill_bf16(head.ptr, V * d, 9, 300, 0.0, 0.02)
+    capi.call("hfmoe_register_lm_head", head.ptr, None, V)
+    x = synth.make_x_dev(T, d, seed=9)
+    out = capi.DeviceBuffer(T * d * 4)
+    xb = capi.DeviceBuffer(T * d * 2)
+    logits = capi.DeviceBuffer(T * V * 4)
+    tok = capi.DeviceBuffer(T * 4)
+    INV, NREG = capi.ERR_INVALID_ARGUMENT, capi.ERR_NOT_REGISTERED
+    cases = [
+        ("MoE: T past max_tokens", lambda: L.hfmoe_moe_forward(0, x.ptr, T + 1, out.ptr, None), INV),
+        ("MoE: T < 0", lambda: L.hfmoe_moe_forward(0, x.ptr, -1, out.ptr, None), INV),
+        ("MoE: null x", lambda: L.hfmoe_moe_forward(0, None, 1, out.ptr, None), INV),
+        ("MoE: x 4-byte aligned", lambda: L.hfmoe_moe_forward(0, x.ptr + 4, 1, out.ptr, None), INV),
+        ("MoE: a dense layer", lambda: L.hfmoe_moe_forward(1, x.ptr, 1, out.ptr, None), INV),
+        ("MoE: T = 0", lambda: L.hfmoe_moe_forward(0, None, 0, None, None), capi.OK),
+        ("BF16 x: T past max_tokens", lambda: L.hfmoe_moe_forward_bf16(0, xb.ptr, T + 1, out.ptr, None), INV),
+        ("BF16 x: null x", lambda: L.hfmoe_moe_forward_bf16(0, None, 1, out.ptr, None), INV),
+        ("BF16 x: x 2-byte aligned", lambda: L.hfmoe_moe_forward_bf16(0, xb.ptr + 2, 1, out.ptr, None), INV),
+        ("dense: T past max_tokens", lambda: L.hfmoe_dense_mlp_forward(1, x.ptr, T + 1, out.ptr, None), INV),
+        ("dense: a MoE layer", lambda: L.hfmoe_dense_mlp_forward(0, x.ptr, 1, out.ptr, None), NREG),
+        ("dense: out 4-byte aligned", lambda: L.hfmoe_dense_mlp_forward(1, x.ptr, 1, out.ptr + 4, None), INV),
+        ("dense: T = 0", lambda: L.hfmoe_dense_mlp_forward(1, None, 0, None, None), capi.OK),
+        ("LM head: T past max_tokens", lambda: L.hfmoe_lm_head(x.ptr, T + 1, logits.ptr, tok.ptr, None), INV),
+        ("LM head: null logits", lambda: L.hfmoe_lm_head(x.ptr, 1, None, tok.ptr, None), INV),
+        ("LM head: h 4-byte aligned", lambda: L.hfmoe_lm_head(x.ptr + 4, 1, logits.ptr, tok.ptr, None), INV),
+        ("block: T past max_tokens", lambda: L.hfmoe_mlp_block(0, x.ptr, T + 1, None), INV),
+        ("block: null h", lambda: L.hfmoe_mlp_block(0, None, 1, None), INV),
+        ("block: h 4-byte aligned", lambda: L.hfmoe_mlp_block(0, x.ptr + 4, 1, None), INV),
+        ("block: unregistered layer", lambda: L.hfmoe_mlp_block(9, x.ptr, 1, None), NREG),
+        ("block: T = 0", lambda: L.hfmoe_mlp_block(0, None, 0, None), capi.OK),
+    ]
+    for what, call, want in cases:
+        rc = call()
+        assert rc == want, (what, rc, L.hfmoe_last_error())
+    capi.call("hfmoe_synchronize")
+    res = r.forward(x, T)
+    xh = x.download(np.float32, T * d).reshape(T, d)
+    for t in range(T):
+        r.check_token(xh[t], res, t)
+    for b in dense + [head, x, out, xb, logits, tok]:
+        b.free()
+    r.free()
