@@ -21,13 +21,16 @@ static bool grouped_supported() {
     return c.d % kGemmTileK == 0 && c.I % kGemmTileK == 0 && c.n_shared <= 1;
 }
 
-// Split-K factor of the router GEMM: enough (tile, split) items for every CU,
-// each split at least 4 K stages long.
+// Split-K factor of the router GEMM: about one (tile, split) item per CU,
+// each split at least 4 K stages long.  (At d = 6144, E = 256: T = 4096 in
+// 4 splits, router GEMM + split sum 58-61 -> 45-47 us against 8, which gave
+// two items per CU; T = 1024 in 16 against 24, 31-32 -> 25-26 us; FP32 x
+// alike.)
 static int router_ksplit(int T) {
     const Cfg& c = g.cfg;
     const int tiles = ((T + kGemmTileRows - 1) / kGemmTileRows) * ((c.E + 127) / 128);
     const int kmax = c.d / kGemmTileK;
-    const int want = (2 * g.num_cus + tiles - 1) / tiles;
+    const int want = (g.num_cus + tiles - 1) / tiles;
     int best = 1;
     for (int ks = 1; ks <= kmax / 4 && ks <= want; ++ks)
         if (kmax % ks == 0) best = ks;
