@@ -647,22 +647,23 @@ __device__ __forceinline__ void gemm_item_split(const GemmArgs& a, int item, uin
         const size_t src = (size_t)(a.a_rowmap ? a.a_rowmap[gr] : gr);
         aoff[j] = (uint32_t)(2 * (src * a.K + kbase + c * 8));
     }
+    // A PARTIAL tile past b_split lies wholly in the second matrix: its
+    // output columns n are rows n - b_split of b_fixed1.
+    const bool second = EPI == EPI_PARTIAL && a.b_split > 0 && n0 >= a.b_split;
+    const int nsub = second ? a.b_split : 0;
 #pragma unroll
     for (int j = 0; j < NBD; ++j) {
         const int i = (wave * NBD + j) * 64 + lane;
         const int r = i >> 3;
         const int c = (i & 7) ^ (r & 7);
         int n = EPI == EPI_SWIGLU ? n0 + r % (32 * CB) : n0 + r;
-        n = min(n, a.N - 1);
+        n = min(n, a.N - 1) - nsub;
         boff[j] = (uint32_t)(2 * ((size_t)n * a.b_ld + kbase + c * 8));
     }
-    // A PARTIAL tile past b_split lies wholly in the second matrix: its rows
-    // n address b_fixed1 from a base b_split rows before it.
-    const uint16_t* bsel = (EPI == EPI_SWIGLU && wave >= 4) ? b1 : b0;
-    if (EPI == EPI_PARTIAL && a.b_split > 0 && n0 >= a.b_split) bsel = b1 - (size_t)a.b_split * a.b_ld;
     // Byte offsets within 4 GiB of each operand's base (every activation and
     // weight buffer of a layer is far smaller).
-    const __amdgpu_buffer_rsrc_t rb = raw_rsrc(uniform_ptr(bsel));
+    const __amdgpu_buffer_rsrc_t rb =
+        raw_rsrc(uniform_ptr(((EPI == EPI_SWIGLU && wave >= 4) || second) ? b1 : b0));
     const __amdgpu_buffer_rsrc_t ra0 = raw_rsrc(a.a_hi);
     const __amdgpu_buffer_rsrc_t ra1 = raw_rsrc(HALVES == 2 ? a.a_lo : a.a_hi);
 
