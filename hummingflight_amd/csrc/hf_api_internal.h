@@ -77,6 +77,7 @@ struct LmHead {
     const uint16_t* norm = nullptr;  // final RMSNorm weight [d] or null
     int vocab = 0;
     void* part = nullptr;            // per-block winners of the T = 1 GEMV
+    int part_n = 0;                  // their number: the most workgroups that GEMV takes
 };
 
 // Buffers of the dense-MLP layers (sized for the largest registered inter).

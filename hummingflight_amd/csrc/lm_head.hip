@@ -173,6 +173,9 @@ hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, int M, int K, f
 }
 
 static int lm_grid() { return env_int("HFMOE_LM_BLOCKS", g.num_cus * 2); }
+// Workgroups of a T = 1 call: HFMOE_LM_BLOCKS as read now, within the
+// per-workgroup winners allocated at registration.
+static int lm_call_grid() { return std::max(1, std::min(lm_grid(), g.lm.part_n)); }
 
 void lm_head_release() {
     if (g.lm.part) hipFree(g.lm.part);
@@ -195,15 +198,16 @@ static int lm_head_forward(const float* h, int T, float* logits, int* token, hip
     HF_CHECK_LAUNCH(launch_rmsnorm(h, L.norm, xn, T, c.d, c.eps, s), "final norm");
     const bool gemm = T > 1 && g.gws.xh && c.d % kGemmTileK == 0;
     if (!gemm) {
+        const int grid = lm_call_grid();
         for (int t = 0; t < T; ++t) {
             prof_begin(p, "lm_head_gemv", s);
             HF_CHECK_LAUNCH(launch_lm_gemv(L.w, xn + (size_t)t * c.d, L.vocab, c.d, logits + (size_t)t * L.vocab,
-                                           static_cast<ArgMax*>(L.part), lm_grid(), s),
+                                           static_cast<ArgMax*>(L.part), grid, s),
                             "lm head gemv");
             if (token) {
                 prof_begin(p, "lm_argmax", s);
                 HF_CHECK_LAUNCH(launch(argmax_merge_kernel, dim3(1), dim3(256), 0, s,
-                                       static_cast<const ArgMax*>(L.part), lm_grid(), token + t),
+                                       static_cast<const ArgMax*>(L.part), grid, token + t),
                                 "argmax");
             }
         }
@@ -257,8 +261,10 @@ int hfmoe_register_lm_head(const uint16_t* lm_head_dev, const uint16_t* final_no
         return fail(HFMOE_ERR_INVALID_ARGUMENT, "lm head must be 16-byte aligned with hidden a multiple of 8");
     if (g.cfg.d > 8192) return fail(HFMOE_ERR_UNSUPPORTED, "hidden %d > 8192", g.cfg.d);
     lm_head_release();
-    hipError_t e = hipMalloc(&g.lm.part, sizeof(ArgMax) * (size_t)lm_grid());
+    const int part_n = std::max(1, lm_grid());
+    hipError_t e = hipMalloc(&g.lm.part, sizeof(ArgMax) * (size_t)part_n);
     if (e != hipSuccess) return fail_hip(e, "lm head workspace");
+    g.lm.part_n = part_n;
     g.lm.w = lm_head_dev;
     g.lm.norm = final_norm_dev;
     g.lm.vocab = vocab;
